@@ -1,0 +1,418 @@
+"""Benchmark of the gfx950 attention path on BASELINE.json's configurations.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg3|cfg2|cfg4|cfg5|all]
+
+Prints ONE JSON line. `value` is BASELINE's headline metric on its headline
+workload: achieved HBM GB/s of Llama-3-8B-shaped paged Q8_0 decode attention
+at batch 64 (config 3), inputs resident in HBM. The other configurations are
+reported under "secondary" (config 2: 32 layers of f32 decode; config 4:
+4x2048 causal prefill in TFLOP/s; config 5: Gemma-2 windowed + global decode).
+
+Timing: W untimed steps, then K steps between two HIP events recorded on the
+library's stream (the stream the kernels run on), with a device
+synchronisation on both sides. A step is one attention call over the whole
+batch (one layer); consecutive steps alternate between layers whose K/V live
+in different memory, so the 256 MB Infinity Cache cannot serve repeats.
+
+cpu_baseline: the C restatement of Glint's CPU flash path (oracle/) on the
+same inputs, on the host cores, parallel over sequences as Glint's Rayon loop
+(src/transformer/forward.rs:1499-1502), on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from glint_amd import _lib, synth  # noqa: E402
+from glint_amd.attn import GpuBackend  # noqa: E402
+
+METRIC = "decode-attn HBM GB/s (% peak) + prefill TFLOP/s, Llama-3-8B GQA shape"
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+PAGE = 16
+SEED = 0x61F7
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class HipEvents:
+    """hipEvent timing on a given stream, through the HIP runtime the library loaded."""
+
+    def __init__(self):
+        self.h = C.CDLL("libamdhip64.so.7")
+        self.h.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.h.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.h.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def create(self):
+        e = C.c_void_p()
+        assert self.h.hipEventCreate(C.byref(e)) == 0
+        return e
+
+    def record(self, e, stream: int) -> None:
+        assert self.h.hipEventRecord(e, C.c_void_p(stream)) == 0
+
+    def elapsed_ms(self, a, b) -> float:
+        assert self.h.hipEventSynchronize(b) == 0
+        ms = C.c_float()
+        assert self.h.hipEventElapsedTime(C.byref(ms), a, b) == 0
+        return float(ms.value)
+
+
+def time_steps(be: GpuBackend, ev: HipEvents, step, steps: int, warmup: int) -> float:
+    """Mean ms per step over `steps` timed steps."""
+    for i in range(warmup):
+        step(i)
+    be.sync()
+    e0, e1 = ev.create(), ev.create()
+    ev.record(e0, be.stream)
+    for i in range(steps):
+        step(warmup + i)
+    ev.record(e1, be.stream)
+    be.sync()
+    return ev.elapsed_ms(e0, e1) / steps
+
+
+def write_pool_chunked(pool, seed_k, seed_v, first_page, n_pages, kv_dim, k_mul=1.0, keep_q8=False):
+    """Generate N(0,1) rows page-chunk by page-chunk, write them (quantise-on-write) and
+    optionally keep the host Q8_0 bytes (Glint's 34-byte blocks) for the CPU baseline."""
+    chunk = max(1, (1 << 16) // PAGE)
+    kq = vq = None
+    if keep_q8:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as orc
+        rb = orc.q8_row_bytes(kv_dim)
+        kq = np.empty((n_pages * PAGE, rb), np.uint8)
+        vq = np.empty_like(kq)
+    for p0 in range(0, n_pages, chunk):
+        n = min(chunk, n_pages - p0)
+        rows, k, v = synth.pool_rows(seed_k, seed_v, first_page + p0, n, kv_dim, k_mul)
+        pool.write_rows(rows, k, v)
+        if keep_q8:
+            kq[p0 * PAGE:(p0 + n) * PAGE] = orc.q8_quantize_rows(k)
+            vq[p0 * PAGE:(p0 + n) * PAGE] = orc.q8_quantize_rows(v)
+    return kq, vq
+
+
+def unique_rows(pb: synth.PagedBatch, table_offset: int = 0) -> tuple[int, int]:
+    """(unique physical rows read, logical rows read) by a decode over pb."""
+    rows = []
+    for b in range(len(pb.ctx)):
+        pos = np.arange(pb.kv_start[b], pb.kv_start[b] + pb.kv_len[b])
+        rows.append((pb.table[b, pos // PAGE].astype(np.int64) + table_offset) * PAGE + pos % PAGE)
+    allr = np.concatenate(rows) if rows else np.zeros(0, np.int64)
+    return int(len(np.unique(allr))), int(len(allr))
+
+
+def pages_read(pb: synth.PagedBatch) -> int:
+    n = 0
+    for b in range(len(pb.ctx)):
+        if pb.kv_len[b] > 0:
+            n += (int(pb.kv_start[b] + pb.kv_len[b] - 1) // PAGE) - int(pb.kv_start[b]) // PAGE + 1
+    return n
+
+
+def cpu_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+# --------------------------------------------------------------------------- decode workloads
+class PagedDecode:
+    """Configs 3 and 5: batched decode over a paged Q8_0 pool, `n_layers` layers in one pool."""
+
+    def __init__(self, be, name, H, Hkv, d, B, ctx_lo, ctx_hi, prefix, softcap, windows, k_mul, seed):
+        self.be, self.name, self.H, self.Hkv, self.d = be, name, H, Hkv, d
+        self.kv_dim = Hkv * d
+        self.scale = float(1.0 / np.sqrt(d))
+        self.softcap = softcap
+        self.ctx = synth.uniform_int(seed, ctx_lo, ctx_hi, B)
+        base = synth.paged_batch(seed + 1, self.ctx, prefix_tokens=prefix)
+        self.n_layers = len(windows)
+        self.layers = []
+        total_pages = base.n_pages * self.n_layers
+        self.pool = be.create_page_pool(total_pages, Hkv, d, "q8")
+        self.host_q8 = None
+        for li, w in enumerate(windows):
+            pb = synth.windowed(base, w)
+            table = pb.table + li * base.n_pages
+            kq, vq = write_pool_chunked(self.pool, synth.tensor_seed(seed, 3, li, 1), synth.tensor_seed(seed, 3, li, 2),
+                                        li * base.n_pages, base.n_pages, self.kv_dim, k_mul, keep_q8=(li == 0))
+            if li == 0:
+                self.host_q8 = (kq, vq, pb)
+            q = synth.normal(synth.tensor_seed(seed, 3, li, 3), (B, H, d))
+            uniq, logical = unique_rows(pb)
+            bytes_kv = uniq * 2 * Hkv * (d + (d // 32) * 2)
+            self.layers.append(dict(
+                pb=pb,
+                q=be.buffer(q), q_host=q, out=be.empty(q.nbytes),
+                start=be.buffer(pb.kv_start), len=be.buffer(pb.kv_len), table=be.buffer(table),
+                stride=table.shape[1], max_len=int(pb.kv_len.max()),
+                bytes=bytes_kv + pages_read(pb) * 4 + 2 * q.nbytes,
+                bytes_logical=logical * 2 * Hkv * (d + (d // 32) * 2) + pages_read(pb) * 4 + 2 * q.nbytes,
+                flops=4 * H * d * int(pb.kv_len.sum()),
+            ))
+        be.sync()
+
+    def step(self, i):
+        L = self.layers[i % self.n_layers]
+        self.be.decode(self.pool, L["q"], L["out"], L["start"], L["len"], len(self.ctx), L["max_len"], self.H,
+                       self.scale, self.softcap, page_table=L["table"], page_table_stride=L["stride"])
+
+    def bytes_per_step(self):
+        return float(np.mean([L["bytes"] for L in self.layers]))
+
+    def cpu_baseline(self, min_seconds=10.0):
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as orc
+        kq, vq, pb = self.host_q8
+        pk = kq.reshape(-1, PAGE, kq.shape[-1])
+        pv = vq.reshape(-1, PAGE, vq.shape[-1])
+        stores = [orc.paged_q8(pk, pv, self.kv_dim, pb.table[b:b + 1]) for b in range(len(self.ctx))]
+        L0 = self.layers[0]
+        q = L0["q_host"].reshape(len(self.ctx), -1)
+        nt = cpu_threads()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            orc.decode_batch(q, stores, 0, pb.kv_start, pb.kv_len, self.H, self.Hkv, self.d, self.scale,
+                             self.softcap, n_threads=nt)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= min_seconds or reps >= 50:
+                break
+        return dict(value=round(L0["bytes"] * reps / el / 1e9, 3), unit="GB/s", cores=nt, kind="port",
+                    sample=f"{reps} x layer 0 of {self.name} (all {len(self.ctx)} sequences, same inputs), "
+                           f"{el:.1f} s")
+
+
+class ContigDecode:
+    """Config 2: single-sequence f32 decode, 32 layers back to back (1 GiB of K/V)."""
+
+    def __init__(self, be, n_layers=32, ctx=4096, H=32, Hkv=8, d=128, seed=0x2222):
+        self.be, self.H, self.Hkv, self.d, self.ctx = be, H, Hkv, d, ctx
+        self.kv_dim = Hkv * d
+        self.n_layers = n_layers
+        self.scale = float(1.0 / np.sqrt(d))
+        self.cache = be.create_kv_cache(n_layers, ctx, Hkv, d, "f32", 1)
+        ppl = (ctx + PAGE - 1) // PAGE
+        self.host = None
+        for layer in range(n_layers):
+            rows = (layer * ppl * PAGE + np.arange(ctx)).astype(np.int64)
+            k = synth.normal_rows(synth.tensor_seed(seed, 2, layer, 1), ctx, self.kv_dim)
+            v = synth.normal_rows(synth.tensor_seed(seed, 2, layer, 2), ctx, self.kv_dim)
+            for i in range(0, ctx, 1 << 14):
+                self.cache.write_rows(rows[i:i + (1 << 14)], k[i:i + (1 << 14)], v[i:i + (1 << 14)])
+            if layer == 0:
+                self.host = (k, v)
+        self.q_host = [synth.normal(synth.tensor_seed(seed, 2, layer, 3), (1, H, d)) for layer in range(n_layers)]
+        self.q = [be.buffer(x) for x in self.q_host]
+        self.out = be.empty(H * d * 4)
+        self.start = be.buffer(np.zeros(1, np.int32))
+        self.len = be.buffer(np.full(1, ctx, np.int32))
+        be.sync()
+
+    def step(self, i):
+        layer = i % self.n_layers
+        self.be.decode(self.cache, self.q[layer], self.out, self.start, self.len, 1, self.ctx, self.H, self.scale,
+                       layer=layer)
+
+    def bytes_per_step(self):
+        return float(2 * self.ctx * self.kv_dim * 4 + 2 * self.H * self.d * 4)
+
+    def cpu_baseline(self, min_seconds=5.0):
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as orc
+        k, v = self.host
+        st = orc.kv_cache(k[None], v[None])
+        q = self.q_host[0].reshape(-1)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            orc.attn_heads_cpu(q, st, 0, 0, self.ctx, self.H, self.H // self.Hkv, self.d, self.scale)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= min_seconds or reps >= 200:
+                break
+        return dict(value=round(self.bytes_per_step() * reps / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                    sample=f"{reps} x layer 0 (attn_heads_cpu, serial over heads as Glint), {el:.1f} s")
+
+
+class Prefill:
+    """Config 4: causal prefill of 4 prompts x 2048, f32 KV cache."""
+
+    def __init__(self, be, precision="f32", B=4, S=2048, H=32, Hkv=8, d=128, seed=0x4444):
+        self.be, self.B, self.S, self.H, self.Hkv, self.d = be, B, S, H, Hkv, d
+        self.precision = precision
+        self.kv_dim = Hkv * d
+        self.scale = float(1.0 / np.sqrt(d))
+        self.n_layers = 2
+        self.cache = be.create_kv_cache(self.n_layers, S, Hkv, d, "f32", B)
+        ppl = (S + PAGE - 1) // PAGE
+        self.host = None
+        self.q = []
+        for layer in range(self.n_layers):
+            for b in range(B):
+                rows = (((b * self.n_layers + layer) * ppl) * PAGE + np.arange(S)).astype(np.int64)
+                k = synth.normal_rows(synth.tensor_seed(seed, 4, layer * 8 + b, 1), S, self.kv_dim)
+                v = synth.normal_rows(synth.tensor_seed(seed, 4, layer * 8 + b, 2), S, self.kv_dim)
+                self.cache.write_rows(rows, k, v)
+                if layer == 0 and b == 0:
+                    self.host = (k, v)
+            qh = synth.normal(synth.tensor_seed(seed, 4, layer, 3), (B * S, H, d))
+            if layer == 0:
+                self.q0_host = qh
+            self.q.append(be.buffer(qh))
+        self.out = be.empty(B * S * H * d * 4)
+        self.q_start = be.buffer(np.arange(B + 1, dtype=np.int32) * S)
+        self.pos = be.buffer(np.zeros(B, np.int32))
+        be.sync()
+
+    def step(self, i):
+        layer = i % self.n_layers
+        self.be.prefill(self.cache, self.q[layer], self.out, self.q_start, self.pos, self.B, self.S, self.H,
+                        self.scale, layer=layer, precision=self.precision)
+
+    def flops_per_step(self):
+        return float(4 * self.B * self.H * self.d * self.S * (self.S + 1) // 2)
+
+    def cpu_baseline(self, rows=256):
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as orc
+        k, v = self.host
+        st = orc.kv_cache(k[None], v[None])
+        # a sample of query rows spread over prompt 0 (cost grows with the position)
+        lp = np.linspace(0, self.S - 1, rows).astype(int)
+        nt = cpu_threads()
+        t0 = time.perf_counter()
+        flops = 0
+        for start in range(0, rows, nt):
+            sel = lp[start:start + nt]
+            # one task per query position, as forward.rs:927-931
+            for p in sel:
+                pass
+            q = self.q0_host[sel].reshape(len(sel), -1)
+            for j, p in enumerate(sel):
+                orc.attn_heads_cpu(q[j], st, 0, 0, int(p) + 1, self.H, self.H // self.Hkv, self.d, self.scale)
+                flops += 4 * self.H * self.d * (int(p) + 1)
+        el = time.perf_counter() - t0
+        return dict(value=round(flops / el / 1e12, 6), unit="TFLOP/s", cores=1, kind="port",
+                    sample=f"{rows} query rows of prompt 0 spread over positions 0..{self.S - 1}, {el:.1f} s")
+
+
+# --------------------------------------------------------------------------- main
+def run_decode(be, ev, wl, steps, warmup, peak=HBM_PEAK_GBS):
+    ms = time_steps(be, ev, wl.step, steps, warmup)
+    gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
+    return ms, gbs, gbs / peak
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="all", choices=["cfg2", "cfg3", "cfg4", "cfg5", "all"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU: the attention path has no multi-GPU leg; "
+                                   "run with --gpus 1"}))
+        return 2
+
+    be = GpuBackend(0)
+    ev = HipEvents()
+    result = {
+        "metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded Xorshift64 + Box-Muller, N(0,1) Q/K/V)",
+    }
+    secondary = {}
+    want = {args.workload} if args.workload != "all" else {"cfg2", "cfg3", "cfg4", "cfg5"}
+
+    if "cfg3" in want:
+        log("cfg3: building paged Q8_0 pool (2 layers, B=64)")
+        wl = PagedDecode(be, "cfg3", 32, 8, 128, 64, 128, 8192, 256, None, [None, None], 1.0, SEED + 3)
+        ms, gbs, frac = run_decode(be, ev, wl.step, args.steps, args.warmup) if False else run_decode(be, ev, wl, args.steps, args.warmup)
+        L0 = wl.layers[0]
+        result.update(value=round(gbs, 2), ms_per_step=round(ms, 5))
+        result["config"] = {
+            "workload": "cfg3: Llama-3-8B decode attention, paged Q8_0 KV, B=64, ctx U[128,8192], 16-token pages, "
+                        "256-token shared prefix, one layer per step (2 layers alternating)",
+            "n_heads": 32, "n_kv_heads": 8, "head_dim": 128, "batch": 64, "kv_format": "q8_0 paged",
+            "sum_ctx": int(wl.ctx.sum()), "bytes_per_step_unique": int(wl.bytes_per_step()),
+            "bytes_per_step_logical": int(np.mean([L["bytes_logical"] for L in wl.layers])),
+        }
+        result["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(frac, 4), "traffic": None,
+                              "kernel": "decode_split_kernel<128,4,q8> + decode_combine_kernel (one step)"}
+        if not args.no_cpu:
+            log("cfg3: CPU baseline (oracle, same inputs)")
+            result["cpu_baseline"] = wl.cpu_baseline()
+        log(f"cfg3: {ms * 1e3:.1f} us/step, {gbs:.1f} GB/s ({100 * frac:.1f}% of peak)")
+        del wl
+    if "cfg2" in want:
+        log("cfg2: building 32-layer f32 cache")
+        wl = ContigDecode(be)
+        ms, gbs, frac = run_decode(be, ev, wl, max(args.steps, 64), args.warmup)
+        secondary["cfg2"] = {"workload": "Llama-3-8B single-sequence decode, f32 contiguous ctx 4096, 32 layers back to back",
+                             "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
+                             "frac_of_hbm_peak": round(frac, 4)}
+        if not args.no_cpu:
+            secondary["cfg2"]["cpu_baseline"] = wl.cpu_baseline()
+        log(f"cfg2: {ms * 1e3:.1f} us/layer, {gbs:.1f} GB/s")
+        del wl
+    if "cfg4" in want:
+        log("cfg4: building 4x2048 prefill")
+        wl = Prefill(be, "f32")
+        ms = time_steps(be, ev, wl.step, max(3, args.steps // 10), min(args.warmup, 2))
+        tf = wl.flops_per_step() / (ms * 1e-3) / 1e12
+        secondary["cfg4_f32"] = {"workload": "Llama-3-8B causal prefill 4x2048, f32 KV cache, fp32 MFMA",
+                                 "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+                                 "frac_of_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+        if not args.no_cpu:
+            secondary["cfg4_f32"]["cpu_baseline"] = wl.cpu_baseline()
+        log(f"cfg4: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
+        if args.workload == "cfg4":
+            result.update(value=round(tf, 3), unit="TFLOP/s", ms_per_step=round(ms, 5))
+            result["config"] = {"workload": secondary["cfg4_f32"]["workload"]}
+            result["roofline"] = {"bound": "mfma", "achieved": round(tf, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
+                                  "unit": "TFLOP/s", "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None}
+        del wl
+    if "cfg5" in want:
+        log("cfg5: building Gemma-2 paged Q8_0 pool (windowed + global layer)")
+        wl = PagedDecode(be, "cfg5", 16, 8, 256, 32, 2048, 8192, 0, 50.0, [4096, None], 3.0, SEED + 5)
+        ms, gbs, frac = run_decode(be, ev, wl, args.steps, args.warmup)
+        secondary["cfg5"] = {"workload": "Gemma-2-9B decode, paged Q8_0, B=32, ctx U[2048,8192], soft-cap 50, "
+                                         "window 4096 and global layers alternating",
+                             "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
+                             "frac_of_hbm_peak": round(frac, 4)}
+        log(f"cfg5: {ms * 1e3:.1f} us/layer, {gbs:.1f} GB/s")
+        del wl
+    if result["value"] is None and args.workload in ("cfg2", "cfg5"):
+        s = secondary[args.workload]
+        result.update(value=s["value"], ms_per_step=s["us_per_layer"] / 1e3)
+        result["config"] = {"workload": s["workload"]}
+        result["roofline"] = {"bound": "hbm", "achieved": s["value"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": s["frac_of_hbm_peak"], "traffic": None}
+    if secondary:
+        result["secondary"] = secondary
+    print(json.dumps(result), flush=True)
+    be.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,94 @@
+"""Build recipe for the gfx950 attention library and its host helpers.
+
+    python -m glint_amd.build            # everything
+    python -m glint_amd.build --hip      # libglint_attn.so only
+
+Outputs (in-tree, git-ignored, shipped with the tree to the GPU box):
+    glint_amd/libglint_attn.so    HIP kernels + C ABI (include/glint_attn.h)
+    glint_amd/libglint_synth.so   seeded synthetic inputs (host C)
+    oracle/liboracle.so           CPU oracle, built by oracle/Makefile (tests only)
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+HIP_LIB = PKG / "libglint_attn.so"
+SYNTH_LIB = PKG / "libglint_synth.so"
+ORACLE_DIR = ROOT / "oracle"
+ORACLE_LIB = ORACLE_DIR / "liboracle.so"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+# -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 anywhere in the device code.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{ROOT / 'include'}",
+]
+HIP_SOURCES = ["gla_capi.hip", "gla_kvstore.hip", "gla_decode.hip", "gla_prefill.hip"]
+
+
+def _run(cmd: list[str], cwd: Path | None = None) -> None:
+    proc = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+
+
+def build_hip(jobs: int = 4) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    objs = []
+    cmds = []
+    for src in HIP_SOURCES:
+        obj = BUILD / (Path(src).stem + ".o")
+        objs.append(obj)
+        cmds.append([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(_run, cmds))
+    tmp = HIP_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    os.replace(tmp, HIP_LIB)
+    return HIP_LIB
+
+
+def build_synth() -> Path:
+    tmp = SYNTH_LIB.with_suffix(".so.tmp")
+    _run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-Wall", "-o", str(tmp), str(CSRC / "synth.c"),
+          "-lm", "-pthread"])
+    os.replace(tmp, SYNTH_LIB)
+    return SYNTH_LIB
+
+
+def build_oracle() -> Path:
+    _run(["make", "-s", "-B", "-C", str(ORACLE_DIR)])
+    return ORACLE_LIB
+
+
+def build_all(jobs: int = 4) -> None:
+    build_synth()
+    build_oracle()
+    build_hip(jobs)
+
+
+if __name__ == "__main__":
+    args = set(sys.argv[1:])
+    if "--hip" in args:
+        build_hip()
+    elif "--host" in args:
+        build_synth()
+        build_oracle()
+    else:
+        build_all()
+    print("built:", ", ".join(str(p.relative_to(ROOT)) for p in (HIP_LIB, SYNTH_LIB, ORACLE_LIB) if p.exists()))

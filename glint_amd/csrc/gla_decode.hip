@@ -1,0 +1,538 @@
+// gla_decode.hip -- single-token decode attention for gfx950 (HBM-bound).
+//
+// Math: flash_attn_1d_ext (src/tensor/flash.rs:46-124) for every q-head of a
+// batch, as attn_heads_cpu runs it (src/transformer/forward.rs:240-270).
+//
+// Work decomposition (split-K / flash-decoding):
+//   grid = (split, kv_head x head_group, sequence), 256 threads (4 waves).
+//   A workgroup owns `pps` consecutive pages of one sequence and one KV head,
+//   and all GT q-heads that read that KV head (GQA: K/V are read once for the
+//   whole group). Each wave takes whole pages; inside a wave 8 lanes share a
+//   token row (each lane owns D/8 elements, loaded as 16-byte chunks so 8
+//   lanes cover 128 contiguous bytes) and the 8 lane groups take 8 different
+//   tokens. A lane group keeps its own online-softmax state (m, l, acc) in
+//   the log2 domain; the groups are merged with shuffles once per split, the
+//   4 waves through LDS, and splits by decode_combine_kernel.
+//   Q8_0 blocks are dequantised in registers: the lane's chunk lies inside
+//   one 32-element block, so the block scale multiplies the partial dot once.
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+
+#include <algorithm>
+
+#include "gla_internal.h"
+
+namespace gla {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct DecodeParams {
+    KvLayout kv;
+    PageMap pm;
+    const int32_t *kv_start;
+    const int32_t *kv_len;
+    const float *q;
+    float *out;
+    float *part_acc;  // [unit][split][GT][D]
+    float *part_ml;   // [unit][split][GT][2]
+    int n_heads;
+    int n_kv_heads;
+    int group;  // n_heads / n_kv_heads
+    int n_hg;   // head groups per kv head
+    int pps;    // pages per split
+    int max_splits;
+    int max_len;  // host bound on kv_len: lengths are clamped to it, so splits never exceed max_splits
+    float q_mul;    // multiplier folded into q: scale*log2(e), or scale with a soft-cap
+    float softcap;  // > 0: cap * tanh(s / cap)
+};
+
+// Sum over the 8 lanes of an aligned lane group (DPP: quad xor1, quad xor2,
+// half-row mirror).
+__device__ __forceinline__ float sum8(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
+    return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// tanh(x) = sign(x) (1 - t) / (1 + t), t = exp(-2|x|).
+__device__ __forceinline__ float tanh_approx(float x) {
+    float t = fast_exp2(-2.0f * kLog2e * fabsf(x));
+    float r = (1.0f - t) / (1.0f + t);
+    return copysignf(r, x);
+}
+
+// Range of pages and splits of sequence b, after clamping to the storage.
+struct SeqRange {
+    int start, end;  // positions [start, end)
+    int fp;          // first logical page
+    int n_pages;
+    int n_splits;
+};
+
+__device__ __forceinline__ SeqRange seq_range(const DecodeParams &p, int b) {
+    SeqRange r;
+    int s = p.kv_start[b];
+    int len = p.kv_len[b];
+    s = s < 0 ? 0 : s;
+    len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
+    int e = s + len;
+    if (e > p.pm.pos_limit) e = p.pm.pos_limit;
+    if (s > e) s = e;
+    r.start = s;
+    r.end = e;
+    if (e > s) {
+        r.fp = s >> 4;
+        r.n_pages = ((e - 1) >> 4) - r.fp + 1;
+        r.n_splits = (r.n_pages + p.pps - 1) / p.pps;
+    } else {
+        r.fp = 0;
+        r.n_pages = 0;
+        r.n_splits = 0;
+    }
+    return r;
+}
+
+template <int CB>
+struct Chunk;
+template <>
+struct Chunk<16> {
+    using T = uint4;
+};
+template <>
+struct Chunk<8> {
+    using T = uint2;
+};
+
+template <int CB>
+__device__ __forceinline__ typename Chunk<CB>::T zero_chunk();
+template <>
+__device__ __forceinline__ uint4 zero_chunk<16>() {
+    return make_uint4(0, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ uint2 zero_chunk<8>() {
+    return make_uint2(0, 0);
+}
+
+__device__ __forceinline__ uint32_t chunk_word(const uint4 &c, int w) {
+    return w == 0 ? c.x : (w == 1 ? c.y : (w == 2 ? c.z : c.w));
+}
+__device__ __forceinline__ uint32_t chunk_word(const uint2 &c, int w) { return w == 0 ? c.x : c.y; }
+
+// Element e of a chunk as float: f32 chunks hold 4 floats, Q8 chunks 8 or 16
+// signed bytes.
+template <bool Q8, typename T>
+__device__ __forceinline__ float chunk_elem(const T &c, int e) {
+    if constexpr (Q8) {
+        uint32_t w = chunk_word(c, e >> 2);
+        return (float)(int8_t)((w >> ((e & 3) * 8)) & 0xff);
+    } else {
+        return __uint_as_float(chunk_word(c, e));
+    }
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+
+template <int D, int GT, bool Q8, int NSTEP>
+__global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodeParams p) {
+    constexpr int EPL = D / 8;                    // elements per lane
+    constexpr int CB = (Q8 && D == 64) ? 8 : 16;  // bytes per chunk load
+    constexpr int EPC = Q8 ? CB : CB / 4;         // elements per chunk
+    constexpr int NCH = EPL / EPC;                // chunks per lane
+    constexpr int PPW = NSTEP / 2;                // pages per wave per iteration
+    using CT = typename Chunk<CB>::T;
+
+    __shared__ float lds_acc[kWaves][GT][D];
+    __shared__ float lds_m[kWaves][GT];
+    __shared__ float lds_l[kWaves][GT];
+
+    const int split = blockIdx.x;
+    const int b = blockIdx.z;
+    const int kvh = blockIdx.y / p.n_hg;
+    const int hg = blockIdx.y - kvh * p.n_hg;
+    const int g0 = hg * GT;
+    const int gcount = min(GT, p.group - g0);
+    const int h_base = kvh * p.group + g0;
+
+    const SeqRange r = seq_range(p, b);
+    const int tid = threadIdx.x;
+    if (r.n_pages == 0) {  // empty window: zero output (the reference's pre-zeroed buffer)
+        if (split == 0)
+            for (int idx = tid; idx < gcount * D; idx += kThreads)
+                p.out[((int64_t)b * p.n_heads + h_base) * D + idx] = 0.0f;
+        return;
+    }
+    if (split >= r.n_splits) return;
+    const int pg0 = r.fp + split * p.pps;
+    const int pg1 = min(r.fp + r.n_pages, pg0 + p.pps);
+
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int tg = lane >> 3;
+    const int sub = lane & 7;
+
+    // q for the GT heads, in the lane's element order: chunk i covers
+    // elements (i*8 + sub)*EPC .. +EPC.
+    float qv[GT][EPL];
+#pragma unroll
+    for (int g = 0; g < GT; g++) {
+        const int gg = g < gcount ? g : gcount - 1;
+        const float *qp = p.q + ((int64_t)b * p.n_heads + h_base + gg) * D;
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+#pragma unroll
+            for (int e = 0; e < EPC; e++) qv[g][i * EPC + e] = qp[(i * 8 + sub) * EPC + e] * p.q_mul;
+        }
+    }
+
+    float m[GT], l[GT], acc[GT][EPL];
+#pragma unroll
+    for (int g = 0; g < GT; g++) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) acc[g][e] = 0.0f;
+    }
+
+    const int64_t head_off = (int64_t)kvh * p.kv.head_stride;
+
+    for (int pb = pg0 + wave * PPW; pb < pg1; pb += kWaves * PPW) {
+        CT kr[NSTEP][NCH], vr[NSTEP][NCH];
+        float ks[NSTEP][NCH], vs[NSTEP][NCH];
+        bool valid[NSTEP];
+        int64_t pid[PPW];
+#pragma unroll
+        for (int j = 0; j < PPW; j++) pid[j] = map_page(p.pm, b, (pb + j < pg1) ? pb + j : pb);
+#pragma unroll
+        for (int s = 0; s < NSTEP; s++) {
+            const int page = pb + s / 2;
+            const int slot = (s & 1) * 8 + tg;
+            const int pos = page * 16 + slot;
+            valid[s] = page < pg1 && pos >= r.start && pos < r.end;
+            const int64_t base = pid[s / 2] * p.kv.page_stride + head_off + (int64_t)slot * p.kv.row_stride;
+            const uint8_t *kp = p.kv.k + base;
+            const uint8_t *vp = p.kv.v + base;
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                kr[s][i] = *reinterpret_cast<const CT *>(kp + (i * 8 + sub) * CB);
+                vr[s][i] = *reinterpret_cast<const CT *>(vp + (i * 8 + sub) * CB);
+            }
+            if constexpr (Q8) {
+                const int64_t sbase = pid[s / 2] * p.kv.page_stride + head_off + (int64_t)slot * p.kv.srow_stride;
+#pragma unroll
+                for (int i = 0; i < NCH; i++) {
+                    const int blk = ((i * 8 + sub) * EPC) >> 5;
+                    ks[s][i] = half_bits_to_float(*reinterpret_cast<const uint16_t *>(p.kv.ks + sbase + blk * 2));
+                    vs[s][i] = half_bits_to_float(*reinterpret_cast<const uint16_t *>(p.kv.vs + sbase + blk * 2));
+                }
+            }
+        }
+
+        // scores of the NSTEP tokens of this lane group, log2 domain
+        float t[NSTEP][GT];
+#pragma unroll
+        for (int s = 0; s < NSTEP; s++) {
+            float dot[GT];
+#pragma unroll
+            for (int g = 0; g < GT; g++) dot[g] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                float part[GT];
+#pragma unroll
+                for (int g = 0; g < GT; g++) part[g] = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPC; e++) {
+                    const float kf = chunk_elem<Q8>(kr[s][i], e);
+#pragma unroll
+                    for (int g = 0; g < GT; g++) part[g] = fmaf(qv[g][i * EPC + e], kf, part[g]);
+                }
+#pragma unroll
+                for (int g = 0; g < GT; g++) {
+                    if constexpr (Q8)
+                        dot[g] = fmaf(part[g], ks[s][i], dot[g]);
+                    else
+                        dot[g] += part[g];
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < GT; g++) {
+                float x = sum8(dot[g]);
+                if (p.softcap > 0.0f) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
+                t[s][g] = x;
+            }
+        }
+
+        // running maximum; rescale only when it grows
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+            float mx = m[g];
+#pragma unroll
+            for (int s = 0; s < NSTEP; s++)
+                if (valid[s]) mx = fmaxf(mx, t[s][g]);
+            if (mx > m[g]) {
+                const float rs = fast_exp2(m[g] - mx);
+                l[g] *= rs;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) acc[g][e] *= rs;
+                m[g] = mx;
+            }
+        }
+
+        // P . V
+#pragma unroll
+        for (int s = 0; s < NSTEP; s++) {
+            if (!valid[s]) {
+#pragma unroll
+                for (int i = 0; i < NCH; i++) {
+                    vr[s][i] = zero_chunk<CB>();
+                    if constexpr (Q8) vs[s][i] = 0.0f;
+                }
+            }
+            float pw[GT];
+#pragma unroll
+            for (int g = 0; g < GT; g++) {
+                pw[g] = valid[s] ? fast_exp2(t[s][g] - m[g]) : 0.0f;
+                l[g] += pw[g];
+            }
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                float pv[GT];
+#pragma unroll
+                for (int g = 0; g < GT; g++) pv[g] = Q8 ? pw[g] * vs[s][i] : pw[g];
+#pragma unroll
+                for (int e = 0; e < EPC; e++) {
+                    const float vf = chunk_elem<Q8>(vr[s][i], e);
+#pragma unroll
+                    for (int g = 0; g < GT; g++) acc[g][i * EPC + e] = fmaf(pv[g], vf, acc[g][i * EPC + e]);
+                }
+            }
+        }
+    }
+
+    // merge the 8 lane groups of the wave (lanes with equal `sub` own the
+    // same elements)
+#pragma unroll
+    for (int g = 0; g < GT; g++) {
+        float M = m[g];
+        M = fmaxf(M, __shfl_xor(M, 8));
+        M = fmaxf(M, __shfl_xor(M, 16));
+        M = fmaxf(M, __shfl_xor(M, 32));
+        const float f = (m[g] == -INFINITY) ? 0.0f : fast_exp2(m[g] - M);
+        float lg = l[g] * f;
+        lg += __shfl_xor(lg, 8);
+        lg += __shfl_xor(lg, 16);
+        lg += __shfl_xor(lg, 32);
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            float a = acc[g][e] * f;
+            a += __shfl_xor(a, 8);
+            a += __shfl_xor(a, 16);
+            a += __shfl_xor(a, 32);
+            acc[g][e] = a;
+        }
+        m[g] = M;
+        l[g] = lg;
+    }
+    if (lane < 8) {
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+#pragma unroll
+            for (int i = 0; i < NCH; i++)
+#pragma unroll
+                for (int e = 0; e < EPC; e++) lds_acc[wave][g][(i * 8 + sub) * EPC + e] = acc[g][i * EPC + e];
+            if (lane == 0) {
+                lds_m[wave][g] = m[g];
+                lds_l[wave][g] = l[g];
+            }
+        }
+    }
+    __syncthreads();
+
+    // merge the 4 waves; write the output or this split's partial
+    const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
+    for (int idx = tid; idx < gcount * D; idx += kThreads) {
+        const int g = idx / D;
+        const int e = idx - g * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, lds_m[w][g]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            const float mw = lds_m[w][g];
+            const float f = (mw == -INFINITY) ? 0.0f : fast_exp2(mw - M);
+            L = fmaf(lds_l[w][g], f, L);
+            A = fmaf(lds_acc[w][g][e], f, A);
+        }
+        if (r.n_splits == 1) {
+            p.out[((int64_t)b * p.n_heads + h_base + g) * D + e] = L > 0.0f ? A * (1.0f / L) : 0.0f;
+        } else {
+            const int64_t slot = unit * p.max_splits + split;
+            p.part_acc[(slot * GT + g) * D + e] = A;
+            if (e == 0) {
+                p.part_ml[(slot * GT + g) * 2 + 0] = M;
+                p.part_ml[(slot * GT + g) * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// Log-sum-exp merge of the split partials of one (sequence, kv head, head
+// group).
+template <int D, int GT>
+__global__ __launch_bounds__(kThreads) void decode_combine_kernel(const DecodeParams p) {
+    const int b = blockIdx.z;
+    const int kvh = blockIdx.y / p.n_hg;
+    const int hg = blockIdx.y - kvh * p.n_hg;
+    const int g0 = hg * GT;
+    const int gcount = min(GT, p.group - g0);
+    const int h_base = kvh * p.group + g0;
+    const SeqRange r = seq_range(p, b);
+    if (r.n_splits <= 1) return;
+    const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
+    const int64_t slot0 = unit * p.max_splits;
+    for (int idx = threadIdx.x; idx < gcount * D; idx += kThreads) {
+        const int g = idx / D;
+        const int e = idx - g * D;
+        float M = -INFINITY;
+        for (int s = 0; s < r.n_splits; s++) M = fmaxf(M, p.part_ml[((slot0 + s) * GT + g) * 2]);
+        float L = 0.0f, A = 0.0f;
+        for (int s = 0; s < r.n_splits; s++) {
+            const float ms = p.part_ml[((slot0 + s) * GT + g) * 2];
+            const float f = (ms == -INFINITY) ? 0.0f : fast_exp2(ms - M);
+            L = fmaf(p.part_ml[((slot0 + s) * GT + g) * 2 + 1], f, L);
+            A = fmaf(p.part_acc[((slot0 + s) * GT + g) * D + e], f, A);
+        }
+        p.out[((int64_t)b * p.n_heads + h_base + g) * D + e] = L > 0.0f ? A * (1.0f / L) : 0.0f;
+    }
+}
+
+template <int D, int GT, bool Q8>
+int launch_typed(gla_ctx *ctx, const DecodeParams &prm, dim3 grid, bool combine) {
+    constexpr int NSTEP = Q8 ? 4 : 2;
+    hipLaunchKernelGGL((decode_split_kernel<D, GT, Q8, NSTEP>), grid, dim3(kThreads), 0, ctx->stream, prm);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "decode_split_kernel launch: %s", hipGetErrorString(e));
+    if (combine) {
+        hipLaunchKernelGGL((decode_combine_kernel<D, GT>), dim3(1, grid.y, grid.z), dim3(kThreads), 0, ctx->stream,
+                           prm);
+        e = hipGetLastError();
+        if (e != hipSuccess)
+            return set_error(GLA_ERR_KERNEL, "decode_combine_kernel launch: %s", hipGetErrorString(e));
+    }
+    return GLA_OK;
+}
+
+template <int D, int GT>
+int launch_dtype(gla_ctx *ctx, bool q8, const DecodeParams &prm, dim3 grid, bool combine) {
+    return q8 ? launch_typed<D, GT, true>(ctx, prm, grid, combine)
+              : launch_typed<D, GT, false>(ctx, prm, grid, combine);
+}
+
+// Head-group width: the registers of a lane hold GT*(D/8) q values and as
+// many accumulators, so GT*D <= 512.
+int pick_gt(int d, int group) {
+    const int cap = 512 / d;  // 8, 4, 2
+    static const int opts[] = {1, 2, 3, 4, 8};
+    for (int o : opts)
+        if (o <= cap && o >= group) return o;
+    return cap;
+}
+
+template <int D>
+int launch_d(gla_ctx *ctx, int gt, bool q8, const DecodeParams &prm, dim3 grid, bool combine) {
+    switch (gt) {
+    case 1:
+        return launch_dtype<D, 1>(ctx, q8, prm, grid, combine);
+    case 2:
+        return launch_dtype<D, 2>(ctx, q8, prm, grid, combine);
+    case 3:
+        if constexpr (D <= 128) return launch_dtype<D, 3>(ctx, q8, prm, grid, combine);
+        break;
+    case 4:
+        if constexpr (D <= 128) return launch_dtype<D, 4>(ctx, q8, prm, grid, combine);
+        break;
+    case 8:
+        if constexpr (D <= 64) return launch_dtype<D, 8>(ctx, q8, prm, grid, combine);
+        break;
+    }
+    return set_error(GLA_ERR_INVALID, "no decode kernel for head_dim %d and head group %d", D, gt);
+}
+
+}  // namespace
+
+int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
+    const int D = d.head_dim;
+    const int group = d.n_heads / d.n_kv_heads;
+    const int gt = pick_gt(D, group);
+    const int n_hg = (group + gt - 1) / gt;
+    const int ppw = d.q8 ? 2 : 1;  // pages per wave per iteration (NSTEP / 2)
+
+    // pages a window can span (a start inside a page adds one)
+    const int max_pages = d.max_kv_len > 0 ? (d.max_kv_len + GLA_PAGE_SIZE - 1) / GLA_PAGE_SIZE + 1 : 1;
+    const int64_t units = (int64_t)d.n_seqs * d.n_kv_heads * n_hg;
+    // Aim for about 8 workgroups per CU over the longest sequence; every wave
+    // of a split gets at least one iteration.
+    const int64_t target = 8LL * std::max(ctx->n_cu, 1);
+    int64_t splits_t = std::max<int64_t>(1, (target + units - 1) / units);
+    int pps = (int)std::max<int64_t>(1, (max_pages + splits_t - 1) / splits_t);
+    const int quantum = kWaves * ppw;
+    pps = (pps + quantum - 1) / quantum * quantum;
+    if (const char *env = getenv("GLA_DECODE_PPS")) {
+        int v = atoi(env);
+        if (v > 0) pps = v;
+    }
+    const int max_splits = (max_pages + pps - 1) / pps;
+
+    DecodeParams prm;
+    prm.kv = d.kv;
+    prm.pm = d.pm;
+    prm.kv_start = d.kv_start;
+    prm.kv_len = d.kv_len;
+    prm.q = d.q;
+    prm.out = d.out;
+    prm.n_heads = d.n_heads;
+    prm.n_kv_heads = d.n_kv_heads;
+    prm.group = group;
+    prm.n_hg = n_hg;
+    prm.pps = pps;
+    prm.max_splits = max_splits;
+    prm.max_len = d.max_kv_len;
+    const bool cap = d.softcap > 0.0f;
+    prm.q_mul = cap ? d.scale : d.scale * kLog2e;
+    prm.softcap = cap ? d.softcap : 0.0f;
+    prm.part_acc = nullptr;
+    prm.part_ml = nullptr;
+    if (max_splits > 1) {
+        const size_t slots = (size_t)units * max_splits;
+        const size_t acc_b = slots * gt * D * sizeof(float);
+        const size_t ml_b = slots * gt * 2 * sizeof(float);
+        int rc = ensure_scratch(ctx, acc_b + ml_b);
+        if (rc != GLA_OK) return rc;
+        prm.part_acc = (float *)ctx->scratch;
+        prm.part_ml = (float *)((uint8_t *)ctx->scratch + acc_b);
+    }
+    if (d.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "decode: n_seqs %d > 65535", d.n_seqs);
+    dim3 grid(max_splits, d.n_kv_heads * n_hg, d.n_seqs);
+    switch (D) {
+    case 64:
+        return launch_d<64>(ctx, gt, d.q8, prm, grid, max_splits > 1);
+    case 128:
+        return launch_d<128>(ctx, gt, d.q8, prm, grid, max_splits > 1);
+    case 256:
+        return launch_d<256>(ctx, gt, d.q8, prm, grid, max_splits > 1);
+    }
+    return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
+}
+
+}  // namespace gla

@@ -1,0 +1,172 @@
+// gla_internal.h -- shared definitions of the gfx950 attention library.
+//
+// Device layout of KV storage (contiguous caches and pools alike).
+// Everything is a page of GLA_PAGE_SIZE (16) positions of one layer; a
+// contiguous cache of (n_seqs, n_layers, max_seq) is the page range
+//   page = (seq * n_layers + layer) * pages_per_layer + pos / 16
+// so one kernel family reads both. Within a page the heads are contiguous
+// chunks ("head-major"), so one (page, kv head) is a single span of HBM:
+//
+//   f32 : [page][kv_head] { K[16][d] f32 | V[16][d] f32 }            128*d B per head
+//   Q8_0: [page][kv_head] { Kq[16][d] i8 | Vq[16][d] i8 |
+//                           Ks[16][d/32] f16 | Vs[16][d/32] f16 }    34*d B per head
+//
+// The Q8_0 split of quants and scales keeps every quant row 16-byte aligned
+// (Glint's 34-byte block, src/cache/mod.rs:276, is not); the byte count per
+// position is unchanged (34 per 32 elements) and export re-packs the blocks.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/glint_attn.h"
+
+#define GLA_CHECK_HIP(expr, code)                                                                   \
+    do {                                                                                            \
+        hipError_t _e = (expr);                                                                     \
+        if (_e != hipSuccess) return gla::set_error((code), "%s: %s", #expr, hipGetErrorString(_e)); \
+    } while (0)
+
+namespace gla {
+
+int set_error(int code, const char *fmt, ...);
+void clear_error();
+
+// Byte strides of a KV layout. Element (page, head, slot, i) of K sits at
+//   k + page * page_stride + head * head_stride + slot * row_stride + i * esize
+// and its Q8_0 scale (block i / 32) at
+//   ks + page * page_stride + head * head_stride + slot * srow_stride + (i / 32) * 2.
+struct KvLayout {
+    const uint8_t *k;
+    const uint8_t *v;
+    const uint8_t *ks;
+    const uint8_t *vs;
+    int64_t page_stride;
+    int64_t head_stride;
+    int32_t row_stride;
+    int32_t srow_stride;
+};
+
+// How a (batch row b, logical page lp) becomes a physical page:
+//   page_table ? page_table[b * pt_stride + lp]
+//              : (seq_slot ? seq_slot[b] : b) * seq_page_stride + layer_page_off + lp
+//
+// The device clamps every index it derives from caller data (positions to
+// [0, pos_limit), sequence slots to [0, n_slots), page ids to [0, n_pages))
+// so a malformed table or length reads wrong data instead of faulting.
+struct PageMap {
+    const int32_t *page_table;
+    const int32_t *seq_slot;
+    int64_t seq_page_stride;
+    int64_t layer_page_off;
+    int64_t n_pages;
+    int32_t pt_stride;
+    int32_t pos_limit;
+    int32_t n_slots;
+};
+
+__device__ __forceinline__ int64_t map_page(const PageMap &pm, int b, int lp) {
+    int64_t id;
+    if (pm.page_table) {
+        id = (int64_t)pm.page_table[(int64_t)b * pm.pt_stride + lp];
+    } else {
+        int64_t s = pm.seq_slot ? (int64_t)pm.seq_slot[b] : (int64_t)b;
+        s = s < 0 ? 0 : (s >= pm.n_slots ? pm.n_slots - 1 : s);
+        id = s * pm.seq_page_stride + pm.layer_page_off + lp;
+    }
+    return id < 0 ? 0 : (id >= pm.n_pages ? pm.n_pages - 1 : id);
+}
+
+}  // namespace gla
+
+struct gla_ctx {
+    int device = 0;
+    int n_cu = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    // split-K partials of decode
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+    // device and pinned host staging of the host-pointer entry points
+    void *dstage = nullptr;
+    size_t dstage_bytes = 0;
+    void *hstage = nullptr;
+    size_t hstage_bytes = 0;
+};
+
+struct gla_kv {
+    gla_ctx *ctx = nullptr;
+    bool is_pool = false;
+    gla_kv_dtype dtype = GLA_KV_F32;
+    int n_kv_heads = 0;
+    int head_dim = 0;
+    int kv_dim = 0;
+    // contiguous caches
+    int n_seqs = 0;
+    int n_layers = 0;
+    int max_seq = 0;
+    int pages_per_layer = 0;
+    int64_t n_pages = 0;
+    int64_t head_bytes = 0;
+    int64_t page_bytes = 0;
+    uint8_t *base = nullptr;
+};
+
+namespace gla {
+
+KvLayout layout_of(const gla_kv *kv);
+int ensure_scratch(gla_ctx *ctx, size_t bytes);
+int ensure_dstage(gla_ctx *ctx, size_t bytes);
+int ensure_hstage(gla_ctx *ctx, size_t bytes);
+
+// Launchers (return GLA_OK or an error code with the message set).
+struct DecodeLaunch {
+    KvLayout kv;
+    bool q8;
+    int head_dim;
+    int n_kv_heads;
+    PageMap pm;
+    int n_seqs;
+    const int32_t *kv_start;
+    const int32_t *kv_len;
+    int max_kv_len;
+    int n_heads;
+    float scale;
+    float softcap;
+    const float *q;
+    float *out;
+};
+int launch_decode(gla_ctx *ctx, const DecodeLaunch &d);
+
+struct PrefillLaunch {
+    KvLayout kv;
+    bool q8;
+    int head_dim;
+    int n_kv_heads;
+    PageMap pm;
+    int n_seqs;
+    const int32_t *q_start;
+    const int32_t *pos_offset;
+    int max_q_len;
+    int n_heads;
+    float scale;
+    float softcap;
+    int sliding_window;
+    gla_precision precision;
+    const float *q;
+    float *out;
+};
+int launch_prefill(gla_ctx *ctx, const PrefillLaunch &p);
+
+int launch_write_rows(gla_ctx *ctx, gla_kv *kv, const int64_t *rows, const float *k, const float *v, int n);
+int launch_export_rows(gla_ctx *ctx, const gla_kv *kv, const int64_t *rows, int n, uint8_t *k_out,
+                       uint8_t *v_out);
+int launch_import_rows(gla_ctx *ctx, gla_kv *kv, const int64_t *rows, int n, const uint8_t *k_in,
+                       const uint8_t *v_in);
+int launch_copy_page(gla_ctx *ctx, gla_kv *kv, int64_t src, int64_t dst);
+int launch_zero_pages(gla_ctx *ctx, gla_kv *kv, int64_t first, int64_t count);
+
+}  // namespace gla

@@ -1,0 +1,339 @@
+// gla_prefill.hip -- batched causal prefill attention on MFMA (gfx950).
+//
+// Math: for every query row, flash_attn_1d_ext over [window_start, pos]
+// (src/transformer/forward.rs:927-958, src/tensor/flash.rs:46-124).
+//
+// Tiling. A workgroup (4 waves) owns a block of query rows of one sequence
+// and HPW q-heads that share one KV head; every wave owns 16*NT queries of one
+// head. K/V tiles of KT=32 positions are staged in LDS once per workgroup and
+// read by all waves (GQA reuse). Per wave and tile:
+//   S^T[key][query] = K . Q^T      v_mfma_f32_16x16x4_f32, Q^T held in VGPRs
+//   online softmax per query column (log2 domain)
+//   O^T[d][query]  += V^T . P^T    P^T is the S^T accumulator itself: the
+//                                  k-step i of a 16-key tile takes keys
+//                                  {4j + i}, j = lane / 16, which is exactly
+//                                  what accumulator register i holds.
+// Permuting the reduction index this way costs nothing and avoids any
+// register shuffle between the two products.
+#include <math.h>
+
+#include "gla_internal.h"
+
+namespace gla {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int KT = 32;  // keys per tile
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+struct PrefillParams {
+    KvLayout kv;
+    PageMap pm;
+    const int32_t *q_start;
+    const int32_t *pos_offset;
+    const float *q;
+    float *out;
+    int n_heads;
+    int n_kv_heads;
+    int group;
+    int hpw;           // q-heads per workgroup
+    int n_qblocks;     // grid.x
+    int max_q_len;     // per-sequence query counts are clamped to it
+    float q_mul;       // scale*log2(e), or scale with a soft-cap
+    float softcap;     // > 0: cap * tanh(s / cap)
+    int sliding_window;
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float tanh_approx(float x) {
+    float t = fast_exp2(-2.0f * kLog2e * fabsf(x));
+    float r = (1.0f - t) / (1.0f + t);
+    return copysignf(r, x);
+}
+
+__device__ __forceinline__ int window_lo(int pos, int w) {
+    if (w <= 0) return 0;
+    int s = pos - w + 1;
+    return s > 0 ? s : 0;
+}
+
+// Stage K (row stride D+2 floats) and V (row stride D+4 floats) of keys
+// [k0, k0+KT) in LDS as f32; keys outside [klo, khi] are zero.
+template <int D, bool Q8>
+__device__ __forceinline__ void load_tile(const PrefillParams &p, int b, int kvh, int k0, int klo, int khi,
+                                          float *Ks, float *Vs) {
+    constexpr int UNITS = KT * D / 16;  // 16 elements per unit
+    const int64_t head_off = (int64_t)kvh * p.kv.head_stride;
+    for (int u = threadIdx.x; u < UNITS; u += kThreads) {
+        const int key = u / (D / 16);
+        const int c16 = u - key * (D / 16);
+        const int kp = k0 + key;
+        float kf[16], vf[16];
+        if (kp >= klo && kp <= khi) {
+            const int64_t pid = map_page(p.pm, b, kp >> 4);
+            const int slot = kp & 15;
+            const int64_t base = pid * p.kv.page_stride + head_off + (int64_t)slot * p.kv.row_stride;
+            if constexpr (Q8) {
+                const uint4 kq = *reinterpret_cast<const uint4 *>(p.kv.k + base + c16 * 16);
+                const uint4 vq = *reinterpret_cast<const uint4 *>(p.kv.v + base + c16 * 16);
+                const int64_t sb = pid * p.kv.page_stride + head_off + (int64_t)slot * p.kv.srow_stride +
+                                   ((c16 * 16) >> 5) * 2;
+                const float ksc = __half2float(__ushort_as_half(*reinterpret_cast<const uint16_t *>(p.kv.ks + sb)));
+                const float vsc = __half2float(__ushort_as_half(*reinterpret_cast<const uint16_t *>(p.kv.vs + sb)));
+                const uint32_t kw[4] = {kq.x, kq.y, kq.z, kq.w};
+                const uint32_t vw[4] = {vq.x, vq.y, vq.z, vq.w};
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    kf[e] = (float)(int8_t)((kw[e >> 2] >> ((e & 3) * 8)) & 0xff) * ksc;
+                    vf[e] = (float)(int8_t)((vw[e >> 2] >> ((e & 3) * 8)) & 0xff) * vsc;
+                }
+            } else {
+                const float4 *kp4 = reinterpret_cast<const float4 *>(p.kv.k + base) + c16 * 4;
+                const float4 *vp4 = reinterpret_cast<const float4 *>(p.kv.v + base) + c16 * 4;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float4 a = kp4[j];
+                    const float4 c = vp4[j];
+                    kf[4 * j] = a.x;
+                    kf[4 * j + 1] = a.y;
+                    kf[4 * j + 2] = a.z;
+                    kf[4 * j + 3] = a.w;
+                    vf[4 * j] = c.x;
+                    vf[4 * j + 1] = c.y;
+                    vf[4 * j + 2] = c.z;
+                    vf[4 * j + 3] = c.w;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                kf[e] = 0.0f;
+                vf[e] = 0.0f;
+            }
+        }
+        float2 *kd = reinterpret_cast<float2 *>(Ks + key * (D + 2) + c16 * 16);
+#pragma unroll
+        for (int j = 0; j < 8; j++) kd[j] = make_float2(kf[2 * j], kf[2 * j + 1]);
+        float4 *vd = reinterpret_cast<float4 *>(Vs + key * (D + 4) + c16 * 16);
+#pragma unroll
+        for (int j = 0; j < 4; j++) vd[j] = make_float4(vf[4 * j], vf[4 * j + 1], vf[4 * j + 2], vf[4 * j + 3]);
+    }
+}
+
+template <int D, int NT, bool Q8>
+__global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillParams p) {
+    constexpr int QW = 16 * NT;  // queries per wave
+    constexpr int KS = D / 4;    // k-steps of S = K Q^T
+    constexpr int DT = D / 16;   // d tiles of O
+    __shared__ float Ks[KT * (D + 2)];
+    __shared__ float Vs[KT * (D + 4)];
+
+    const int b = blockIdx.z;
+    const int n_hgrp = p.group / p.hpw;
+    const int kvh = blockIdx.y / n_hgrp;
+    const int hgrp = blockIdx.y - kvh * n_hgrp;
+    const int qblk = p.n_qblocks - 1 - (int)blockIdx.x;  // longest rows first
+    const int waves_per_head = 4 / p.hpw;
+    const int qwg = QW * waves_per_head;
+
+    const int row0 = p.q_start[b];
+    const int q_len = min(max(p.q_start[b + 1] - row0, 0), p.max_q_len);
+    const int pos0 = p.pos_offset[b];
+    const int qb0 = qblk * qwg;  // first local query of the workgroup
+    if (qb0 >= q_len) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lrow = lane & 15;
+    const int lgrp = lane >> 4;
+    const int head = kvh * p.group + hgrp * p.hpw + (wave % p.hpw);
+    const int wq0 = qb0 + (wave / p.hpw) * QW;  // first local query of this wave
+
+    // key range of the workgroup
+    const int q_last = min(q_len, qb0 + qwg) - 1;
+    const int khi = min(pos0 + q_last, p.pm.pos_limit - 1);
+    const int klo = window_lo(pos0 + qb0, p.sliding_window);
+
+    // Q^T fragments: qf[nt][s] = Q[query nt*16 + lrow][d = 4s + lgrp]
+    float qf[NT][KS];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int lq = wq0 + nt * 16 + lrow;
+        const bool ok = lq < q_len;
+        const float *qp = p.q + ((int64_t)(row0 + (ok ? lq : 0)) * p.n_heads + head) * D;
+#pragma unroll
+        for (int s = 0; s < KS; s++) qf[nt][s] = ok ? qp[4 * s + lgrp] * p.q_mul : 0.0f;
+    }
+
+    floatx4 o[DT][NT];
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) o[t][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[NT], lpart[NT];
+    int qpos[NT], qlo[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        m[nt] = -INFINITY;
+        lpart[nt] = 0.0f;
+        const int lq = wq0 + nt * 16 + lrow;
+        qpos[nt] = lq < q_len ? pos0 + lq : -1;  // -1: padding query, every key masked
+        qlo[nt] = window_lo(pos0 + lq, p.sliding_window);
+    }
+
+    if (khi >= klo) {
+        for (int k0 = (klo / KT) * KT; k0 <= khi; k0 += KT) {
+            __syncthreads();
+            load_tile<D, Q8>(p, b, kvh, k0, klo, khi, Ks, Vs);
+            __syncthreads();
+
+            // S^T = K . Q^T
+            floatx4 sacc[2][NT];
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) sacc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < KS; s++) {
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++) {
+                    const float a = Ks[(mt * 16 + lrow) * (D + 2) + 4 * s + lgrp];
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++)
+                        sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qf[nt][s], sacc[mt][nt], 0, 0, 0);
+                }
+            }
+
+            // online softmax over this tile, per query column
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int kp = k0 + mt * 16 + 4 * lgrp + i;
+                        float x = sacc[mt][nt][i];
+                        if (p.softcap > 0.0f) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
+                        const bool ok = kp <= qpos[nt] && kp >= qlo[nt] && kp >= klo && kp <= khi;
+                        x = ok ? x : -INFINITY;
+                        sacc[mt][nt][i] = x;
+                        mx = fmaxf(mx, x);
+                    }
+                }
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const float m_new = fmaxf(m[nt], mx);
+                if (m_new == -INFINITY) {
+#pragma unroll
+                    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) sacc[mt][nt][i] = 0.0f;
+                    continue;
+                }
+                const float rs = fast_exp2(m[nt] - m_new);
+                m[nt] = m_new;
+                float ls = 0.0f;
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float pv = fast_exp2(sacc[mt][nt][i] - m_new);
+                        sacc[mt][nt][i] = pv;
+                        ls += pv;
+                    }
+                lpart[nt] = lpart[nt] * rs + ls;
+#pragma unroll
+                for (int t = 0; t < DT; t++) o[t][nt] *= rs;
+            }
+
+            // O^T += V^T . P^T
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float *vrow = Vs + (mt * 16 + 4 * lgrp + i) * (D + 4) + lrow;
+#pragma unroll
+                    for (int t = 0; t < DT; t++) {
+                        const float a = vrow[16 * t];
+#pragma unroll
+                        for (int nt = 0; nt < NT; nt++)
+                            o[t][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, sacc[mt][nt][i], o[t][nt], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+
+    // normalise and store: lane holds O^T[16t + 4*lgrp + r][query lrow]
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        float lt = lpart[nt];
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
+        const int lq = wq0 + nt * 16 + lrow;
+        if (lq >= q_len) continue;
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        float *op = p.out + ((int64_t)(row0 + lq) * p.n_heads + head) * D;
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            const floatx4 v = o[t][nt] * inv;
+            *reinterpret_cast<float4 *>(op + 16 * t + 4 * lgrp) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+}
+
+template <int D, int NT, bool Q8>
+int launch_f32(gla_ctx *ctx, const PrefillParams &prm, dim3 grid) {
+    hipLaunchKernelGGL((prefill_f32_kernel<D, NT, Q8>), grid, dim3(kThreads), 0, ctx->stream, prm);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "prefill_f32_kernel launch: %s", hipGetErrorString(e));
+    return GLA_OK;
+}
+
+}  // namespace
+
+int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
+    const int D = a.head_dim;
+    const int group = a.n_heads / a.n_kv_heads;
+    const int hpw = (group % 4 == 0) ? 4 : ((group % 2 == 0) ? 2 : 1);
+    const int NT = D <= 128 ? 2 : 1;
+    const int qwg = 16 * NT * (4 / hpw);
+    PrefillParams prm;
+    prm.kv = a.kv;
+    prm.pm = a.pm;
+    prm.q_start = a.q_start;
+    prm.pos_offset = a.pos_offset;
+    prm.q = a.q;
+    prm.out = a.out;
+    prm.n_heads = a.n_heads;
+    prm.n_kv_heads = a.n_kv_heads;
+    prm.group = group;
+    prm.hpw = hpw;
+    prm.n_qblocks = (a.max_q_len + qwg - 1) / qwg;
+    prm.max_q_len = a.max_q_len;
+    const bool cap = a.softcap > 0.0f;
+    prm.q_mul = cap ? a.scale : a.scale * kLog2e;
+    prm.softcap = cap ? a.softcap : 0.0f;
+    prm.sliding_window = a.sliding_window;
+    if (a.precision != GLA_PREC_F32)
+        return set_error(GLA_ERR_INVALID, "prefill precision %d not built yet", (int)a.precision);
+    if (a.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "prefill: n_seqs %d > 65535", a.n_seqs);
+    dim3 grid(prm.n_qblocks, a.n_kv_heads * (group / hpw), a.n_seqs);
+    switch (D) {
+    case 64:
+        return a.q8 ? launch_f32<64, 2, true>(ctx, prm, grid) : launch_f32<64, 2, false>(ctx, prm, grid);
+    case 128:
+        return a.q8 ? launch_f32<128, 2, true>(ctx, prm, grid) : launch_f32<128, 2, false>(ctx, prm, grid);
+    case 256:
+        return a.q8 ? launch_f32<256, 1, true>(ctx, prm, grid) : launch_f32<256, 1, false>(ctx, prm, grid);
+    }
+    return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
+}
+
+}  // namespace gla

@@ -1,0 +1,46 @@
+"""Test helpers: an f64 brute-force softmax attention (the textbook definition,
+independent of both the oracle and the kernels) and tolerance checks."""
+from __future__ import annotations
+
+import numpy as np
+
+# fp32 parity bar of the attention path: max abs 1e-4 and max rel 1e-3 (an
+# element passes if it meets either bound, rel measured against |want|).
+ABS_TOL = 1e-4
+REL_TOL = 1e-3
+
+
+def attention_f64(q, K, V, scale, softcap=None):
+    """q [d], K/V [L][d] -> softmax(cap(q.K*scale)).V in float64."""
+    q = np.asarray(q, np.float64)
+    K = np.asarray(K, np.float64)
+    V = np.asarray(V, np.float64)
+    if len(K) == 0:
+        return np.zeros(q.shape[-1])
+    s = K @ q * scale
+    if softcap:
+        s = softcap * np.tanh(s / softcap)
+    w = np.exp(s - s.max())
+    w /= w.sum()
+    return w @ V
+
+
+def assert_close(got, want, abs_tol=ABS_TOL, rel_tol=REL_TOL, what=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    err = np.abs(got - want)
+    bad = err > np.maximum(abs_tol, rel_tol * np.abs(want))
+    if bad.any():
+        i = np.unravel_index(np.argmax(np.where(bad, err, 0)), err.shape)
+        raise AssertionError(f"{what}: {bad.sum()} of {bad.size} outside abs {abs_tol} / rel {rel_tol}; "
+                             f"worst at {i}: got {got[i]!r} want {want[i]!r} (abs err {err[i]:.3g})")
+
+
+def max_errors(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    rel = err / np.maximum(np.abs(want), 1e-30)
+    return float(err.max(initial=0.0)), float(rel.max(initial=0.0))

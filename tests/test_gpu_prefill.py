@@ -1,0 +1,99 @@
+"""Batched causal prefill on the GPU (fp32 MFMA) through the C ABI, against the
+oracle's prefill loop (src/transformer/forward.rs:927-958).
+fp32 bar: max abs 1e-4 / rel 1e-3; indexing bit-exact."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from glint_amd import synth
+from gpu_util import Contig, Pool, run_prefill
+from helpers import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_prefill(store, q, pos_offset, H, Hkv, d, scale, softcap=None, window=None, layer=0):
+    T = q.shape[0]
+    return orc.prefill(q.reshape(T, H * d), store, layer, pos_offset, H, Hkv, d, scale, softcap,
+                       window).reshape(T, H, d)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+@pytest.mark.parametrize("d,H,Hkv", [(128, 8, 2), (64, 9, 3), (256, 4, 2), (128, 4, 4), (64, 16, 2)])
+def test_prefill_varlen_batch(backend, dtype, d, H, Hkv):
+    """Three prompts of different lengths and offsets in one launch (chunked prefill)."""
+    lens = [70, 1, 130]
+    offs = [0, 40, 17]
+    max_seq = max(o + n for o, n in zip(offs, lens))
+    c = Contig(backend, dtype, 3, 2, max_seq, Hkv, d, seed=800 + d + H)
+    q = synth.normal(900 + d, (sum(lens), H, d))
+    q_start = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    scale = 1 / np.sqrt(d)
+    for layer, cap, window in [(0, None, None), (1, 30.0, None), (0, None, 21), (1, 15.0, 64)]:
+        got = run_prefill(backend, c.cache, q, q_start, offs, H, scale, cap, window, layer=layer)
+        for b in range(3):
+            rows = slice(q_start[b], q_start[b + 1])
+            want = _oracle_prefill(c.stores[b], q[rows], offs[b], H, Hkv, d, scale, cap, window, layer)
+            assert_close(got[rows], want, what=f"{dtype} d{d} H{H}/{Hkv} seq{b} layer{layer} cap{cap} w{window}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+def test_prefill_paged(backend, dtype):
+    H, Hkv, d = 8, 2, 128
+    ctx = np.array([100, 37, 260], np.int32)
+    pb = synth.paged_batch(41, ctx, prefix_tokens=32)
+    p = Pool(backend, dtype, pb, Hkv, d, seed=42)
+    # each sequence prefills its last n positions (the first ones are "cached")
+    n = np.array([60, 37, 200], np.int32)
+    offs = ctx - n
+    q = synth.normal(43, (int(n.sum()), H, d))
+    q_start = np.concatenate([[0], np.cumsum(n)]).astype(np.int32)
+    for window in (None, 40):
+        got = run_prefill(backend, p.pool, q, q_start, offs, H, 0.09, None, window, table=pb.table)
+        for b in range(3):
+            rows = slice(q_start[b], q_start[b + 1])
+            want = _oracle_prefill(p.stores[b], q[rows], int(offs[b]), H, Hkv, d, 0.09, None, window)
+            assert_close(got[rows], want, what=f"paged {dtype} seq {b} window {window}")
+
+
+def test_prefill_indexing_is_bit_exact(backend):
+    """K = 0 and small-integer V: out = mean of V over [window(pos), pos] exactly."""
+    H, Hkv, d = 8, 2, 64
+    kv_dim = Hkv * d
+    T = 150
+    r = np.arange(T)[:, None]
+    e = np.arange(kv_dim)[None, :]
+    v = (((r * 131 + e * 7) % 255) - 127).astype(np.float32).reshape(1, 1, T, kv_dim)
+    c = Contig(backend, "f32", 1, 1, T, Hkv, d, k=np.zeros_like(v), v=v)
+    q = synth.normal(4, (T, H, d))
+    for window in (None, 16, 33):
+        got = run_prefill(backend, c.cache, q, [0, T], [0], H, 0.125, None, window)
+        for pos in range(T):
+            lo = 0 if not window else max(0, pos - window + 1)
+            s = v[0, 0, lo:pos + 1].astype(np.float64).sum(0).astype(np.float32)
+            want = s * (np.float32(1.0) / np.float32(pos + 1 - lo))
+            for h in range(H):
+                kvh = h // (H // Hkv)
+                assert np.array_equal(got[pos, h].view(np.uint32), want[kvh * d:(kvh + 1) * d].view(np.uint32)), \
+                    (window, pos, h)
+
+
+def test_cfg4_llama_prefill_4x2048(backend):
+    """BASELINE config 4 at full size (4 prompts x 2048, H32/KV8, d128, f32 KV cache), every
+    16th query row of each prompt against the oracle."""
+    H, Hkv, d, S, B = 32, 8, 128, 2048, 4
+    c = Contig(backend, "f32", B, 1, S, Hkv, d, seed=4004)
+    q = synth.normal(4005, (B * S, H, d))
+    q_start = np.arange(B + 1, dtype=np.int32) * S
+    scale = 1 / np.sqrt(128)
+    got = run_prefill(backend, c.cache, q, q_start, [0] * B, H, scale)
+    for b in range(B):
+        rows = np.arange(b * S, (b + 1) * S)
+        sel = np.arange(b % 16, S, 16)
+        out = np.zeros((len(sel), H, d), np.float32)
+        for i, lp in enumerate(sel):
+            out[i] = orc.attn_heads_cpu(q[b * S + lp].reshape(-1), c.stores[b], 0, 0, lp + 1, H, H // Hkv, d,
+                                        scale).reshape(H, d)
+        assert_close(got[rows[sel]], out, what=f"cfg4 prompt {b}")
