@@ -38,7 +38,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}",
 ]
-HIP_SOURCES = ["gla_capi.hip", "gla_kvstore.hip", "gla_decode.hip", "gla_prefill.hip"]
+HIP_SOURCES = ["gla_capi.hip", "gla_kvstore.hip", "gla_decode.hip", "gla_decode_q8.hip", "gla_prefill.hip"]
 
 
 def _run(cmd: list[str], cwd: Path | None = None) -> None:

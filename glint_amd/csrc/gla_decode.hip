@@ -435,8 +435,8 @@ int launch_typed(gla_ctx *ctx, const DecodeParams &prm, dim3 grid, bool combine)
 
 template <int D, int GT>
 int launch_dtype(gla_ctx *ctx, bool q8, const DecodeParams &prm, dim3 grid, bool combine) {
-    return q8 ? launch_typed<D, GT, true>(ctx, prm, grid, combine)
-              : launch_typed<D, GT, false>(ctx, prm, grid, combine);
+    (void)q8;  // Q8_0 storage goes to the MFMA kernel (gla_decode_q8.hip)
+    return launch_typed<D, GT, false>(ctx, prm, grid, combine);
 }
 
 // Head-group width: the registers of a lane hold GT*(D/8) q values and as
@@ -472,6 +472,7 @@ int launch_d(gla_ctx *ctx, int gt, bool q8, const DecodeParams &prm, dim3 grid, 
 }  // namespace
 
 int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
+    if (d.q8) return launch_decode_q8(ctx, d);
     const int D = d.head_dim;
     const int group = d.n_heads / d.n_kv_heads;
     const int gt = pick_gt(D, group);

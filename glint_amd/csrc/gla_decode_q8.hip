@@ -1,0 +1,662 @@
+// gla_decode_q8.hip -- single-token decode attention over Q8_0 KV storage,
+// with both products on MFMA (gfx950, v_mfma_f32_16x16x32_f16).
+//
+// Math: flash_attn_1d_ext (src/tensor/flash.rs:46-124) for every q-head of a
+// batch, as attn_heads_cpu runs it (src/transformer/forward.rs:240-270), over
+// K/V rows dequantised as KvCacheQ8::dequant_range does (src/cache/mod.rs:318-334):
+// k[d] = int8 * f16 scale of its 32-element block.
+//
+// Why MFMA for an HBM-bound kernel: Q8_0 moves one byte per element, and
+// with G q-heads per KV head every K and V element feeds G multiply-adds.
+// On the VALU that is ~5 instructions per byte at G = 4, more than the vector
+// ALUs retire at HBM speed. Here the VALU only turns bytes into f16 (one
+// instruction per element) and applies per-token scales; the products run on
+// the matrix cores.
+//
+// Exactness. int8 values are exact in f16. q and the probabilities are f32;
+// each is split into two f16 pieces (hi = f16(x), lo = f16(x - hi)) after a
+// power-of-two rescale that puts the largest magnitude in [2^13, 2^14), so
+// hi + lo carries ~22 significant bits and no piece is subnormal where it
+// matters. The MFMA multiplies f16 pairs exactly and accumulates in f32.
+//
+// Work: one wave = one (sequence, KV head, group of <= 4 q-heads, chunk of
+// `ch` pages); a workgroup is 4 independent waves. A step covers two pages
+// (32 positions), the K depth of one P.V MFMA.
+//   S = K . Q   A = K tile (16 positions x one 32-element Q8_0 block), B = Q:
+//               column j = (head (j>>1)&3, piece j&1); columns 8-15 repeat 0-7.
+//               One MFMA per block per page; the block scale multiplies the
+//               per-block partial score of each position.
+//   O += P' . V A = P' (row r = (page r>>3 of the step, head, piece)), B = V
+//               tile (32 positions x 16 d); P'[r][t] = piece of
+//               p[t] * vscale[t][block] * 2^kv. Rows of page 0 are zero on
+//               page-1 positions and vice versa, so a lane builds only the
+//               values of its own page and every lane's S column is exactly
+//               its P' row: no data moves between lanes.
+// The Q8_0 quants are stored in this operand order (gla_internal.h), so each
+// lane's operands for a page are one contiguous D/4-byte span.
+// The 4 waves of a workgroup merge their chunks (log-sum-exp) in LDS; units
+// longer than a workgroup are merged by a second, small kernel.
+#include <math.h>
+#include <stdlib.h>
+
+#include <algorithm>
+
+#include "gla_internal.h"
+
+namespace gla {
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+constexpr int kGT = 4;  // q-heads per wave
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMaxChunks = 64;  // preferred bound on chunks per unit (one merge pass)
+
+struct Q8Params {
+    const uint8_t *base;  // KV storage; a (page, head) block is 34*D bytes
+    int64_t page_stride;
+    int64_t head_stride;
+    PageMap pm;
+    const int32_t *kv_start;
+    const int32_t *kv_len;
+    const float *q;
+    float *out;
+    float *part;   // [unit][max_wg][kGT][D + 2]: O (unnormalised), m, l
+    int n_heads;
+    int n_kv_heads;
+    int group;
+    int n_hg;
+    int ch;  // pages per chunk (even)
+    int max_wg;  // workgroups per unit (partials per unit)
+    int max_len;
+    float q_mul;    // scale*log2(e), or scale with a soft-cap
+    float softcap;  // > 0: cap * tanh(s / cap)
+};
+
+struct Range {
+    int start, end;  // positions [start, end)
+    int fp;          // first logical page
+    int n_pages;
+};
+
+__device__ __forceinline__ Range seq_range(const Q8Params &p, int b) {
+    Range r;
+    int s = p.kv_start[b];
+    int len = p.kv_len[b];
+    s = s < 0 ? 0 : s;
+    len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
+    int e = s + len;
+    if (e > p.pm.pos_limit) e = p.pm.pos_limit;
+    if (s > e) s = e;
+    r.start = s;
+    r.end = e;
+    if (e > s) {
+        r.fp = s >> 4;
+        r.n_pages = ((e - 1) >> 4) - r.fp + 1;
+    } else {
+        r.fp = 0;
+        r.n_pages = 0;
+    }
+    return r;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// tanh(x) = sign(x) (1 - t) / (1 + t), t = exp(-2|x|), with the hardware
+// reciprocal (1 ulp) in place of a full-precision divide.
+__device__ __forceinline__ float tanh_approx(float x) {
+    const float t = fast_exp2(-2.0f * kLog2e * fabsf(x));
+    return copysignf((1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t), x);
+}
+
+// Two int8 (selected from xb = bytes ^ 0x80 by `sel`) -> two exact f16:
+// 0x64XX is 1024 + XX in f16, and XX = x + 128.
+__device__ __forceinline__ half2v i8x2_to_h2(uint32_t xb, uint32_t sel) {
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, xb, sel);
+    return __builtin_bit_cast(half2v, h) - (half2v){(_Float16)1152.0f, (_Float16)1152.0f};
+}
+
+// Four int8 of a dword, in byte order, as halves 0..3 of `o` starting at `at`.
+__device__ __forceinline__ void i8x4_to_h(uint32_t w, half8 &o, int at) {
+    const uint32_t x = w ^ 0x80808080u;
+    const half2v a = i8x2_to_h2(x, 0x04010400u);
+    const half2v c = i8x2_to_h2(x, 0x04030402u);
+    o[at + 0] = a[0];
+    o[at + 1] = a[1];
+    o[at + 2] = c[0];
+    o[at + 3] = c[1];
+}
+
+__device__ __forceinline__ uint32_t word(const uint4 &v, int i) {
+    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// f16 number `i` of a packed array of uint4.
+template <int N>
+__device__ __forceinline__ float half_at(const uint4 (&a)[N], int i) {
+    const uint32_t w = word(a[i >> 3], (i >> 1) & 3);
+    const uint16_t h = (i & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffff);
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ float dpp_swap1(float x) {  // lane ^ 1
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+}
+
+// 2^(14 - e) where x = m * 2^e, m in [0.5, 1): maps max|.| into [2^13, 2^14).
+__device__ __forceinline__ int pow2_exp(float x) {
+    int e = 0;
+    (void)frexpf(x, &e);
+    return e < -100 ? -100 : (e > 100 ? 100 : e);
+}
+
+template <int D>
+struct Raw {
+    static constexpr int NV = D / 64;  // uint4 per lane per (page, head) K or V block
+    static constexpr int NS = D / 64;  // uint4 per lane of 4 positions' scales (4 * D/32 f16)
+    uint4 k[2][NV];
+    uint4 v[2][NV];
+    uint4 ks[2][NS];
+    uint4 vs[NS];  // the lane's P.V page only
+};
+
+template <int D>
+__device__ __forceinline__ void load_step(const Q8Params &p, const uint8_t *head_base, int pid_l, int step,
+                                          int npg, int lane, Raw<D> &r) {
+    constexpr int LB = D / 4;  // quant bytes per lane per page
+    const int pa = 2 * step;
+    const int pb = (pa + 1 < npg) ? pa + 1 : pa;
+    const int ida = __builtin_amdgcn_readlane(pid_l, pa);
+    const int idb = __builtin_amdgcn_readlane(pid_l, pb);
+    const uint8_t *ba = head_base + (int64_t)ida * p.page_stride;
+    const uint8_t *bb = head_base + (int64_t)idb * p.page_stride;
+    const int kg = lane >> 4;
+    const int ph = (lane >> 3) & 1;
+#pragma unroll
+    for (int i = 0; i < Raw<D>::NV; i++) {
+        r.k[0][i] = reinterpret_cast<const uint4 *>(ba + lane * LB)[i];
+        r.k[1][i] = reinterpret_cast<const uint4 *>(bb + lane * LB)[i];
+        r.v[0][i] = reinterpret_cast<const uint4 *>(ba + 16 * D + lane * LB)[i];
+        r.v[1][i] = reinterpret_cast<const uint4 *>(bb + 16 * D + lane * LB)[i];
+    }
+    const int soff = kg * 4 * (D / 32) * 2;  // first of the lane's 4 positions
+#pragma unroll
+    for (int i = 0; i < Raw<D>::NS; i++) {
+        r.ks[0][i] = reinterpret_cast<const uint4 *>(ba + 32 * D + soff)[i];
+        r.ks[1][i] = reinterpret_cast<const uint4 *>(bb + 32 * D + soff)[i];
+        r.vs[i] = reinterpret_cast<const uint4 *>((ph ? bb : ba) + 33 * D + soff)[i];
+    }
+}
+
+template <int D>
+struct StepConst {
+    half8 qb[D / 32];
+    float inv_qs, vsc, softcap, inv_cap;
+    bool cap;
+    int pg0, npg, start, end;
+    int kg, ph;
+    float pf;  // this lane's piece (0: hi, 1: lo) as a float
+};
+
+template <int D>
+struct StepState {
+    floatx4 acc[D / 16];
+    float m;     // running max (log2 domain) of the lane's head
+    float lsum;  // sum of p over this lane's P' positions
+};
+
+// One step: two pages (32 positions) of one (sequence, KV head).
+template <int D>
+__device__ __forceinline__ void step_body(const Raw<D> &cur, int step, const StepConst<D> &c, StepState<D> &st) {
+    constexpr int NB = D / 32;
+    constexpr int ND = D / 16;
+
+    // S = K . Q for both pages: the lane holds positions kg*4 + i of its column
+    float s0[4], s1[4];
+#pragma unroll
+    for (int P = 0; P < 2; P++) {
+        floatx4 cb[NB];
+#pragma unroll
+        for (int blk = 0; blk < NB; blk++) {
+            half8 a;
+            i8x4_to_h(word(cur.k[P][blk >> 1], (blk & 1) * 2), a, 0);
+            i8x4_to_h(word(cur.k[P][blk >> 1], (blk & 1) * 2 + 1), a, 4);
+            cb[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, c.qb[blk], floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float x = 0.0f;
+#pragma unroll
+            for (int blk = 0; blk < NB; blk++) x = fmaf(half_at(cur.ks[P], i * NB + blk), cb[blk][i], x);
+            x *= c.inv_qs;
+            x += dpp_swap1(x);  // hi piece + lo piece
+            if (P == 0)
+                s0[i] = x;
+            else
+                s1[i] = x;
+        }
+    }
+    if (c.cap) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s0[i] = c.softcap * tanh_approx(s0[i] * c.inv_cap) * kLog2e;
+            s1[i] = c.softcap * tanh_approx(s1[i] * c.inv_cap) * kLog2e;
+        }
+    }
+
+    // window / length mask (only a chunk's first and last steps can hold
+    // positions outside [start, end)), running max
+    const int sp = (c.pg0 + 2 * step) * 16;             // first position of the step
+    const int lim1 = min(c.end, (c.pg0 + c.npg) * 16);  // page 1 of the step may be past the chunk
+    if (sp < c.start || sp + 32 > lim1) {               // wave-uniform
+        const int pos0 = sp + c.kg * 4;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s0[i] = (pos0 + i >= c.start && pos0 + i < c.end) ? s0[i] : -INFINITY;
+            s1[i] = (pos0 + 16 + i >= c.start && pos0 + 16 + i < lim1) ? s1[i] : -INFINITY;
+        }
+    }
+    float tmax = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(st.m, tmax);  // finite: page 0 of a step always holds a position
+    const float alpha = fast_exp2(st.m - m_new);
+    st.m = m_new;
+
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pr[i] = fast_exp2((c.ph ? s1[i] : s0[i]) - m_new);
+    st.lsum = st.lsum * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+
+    if (__ballot(alpha != 1.0f)) {
+        // rows kg*4 + {0,1} belong to head (2kg)&3, rows kg*4 + {2,3} to (2kg+1)&3
+        const float aA = __shfl(alpha, ((2 * c.kg) & 3) * 2);
+        const float aB = __shfl(alpha, ((2 * c.kg + 1) & 3) * 2);
+#pragma unroll
+        for (int t = 0; t < ND; t++) {
+            st.acc[t][0] *= aA;
+            st.acc[t][1] *= aA;
+            st.acc[t][2] *= aB;
+            st.acc[t][3] *= aB;
+        }
+    }
+
+    // O += P' . V, one 32-element block (two d tiles) at a time.
+    // v = p * vscale * 2^kv; the lane's piece is f16(v - pf * f16(v)).
+    float pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pv[i] = pr[i] * c.vsc;
+#pragma unroll
+    for (int blk = 0; blk < NB; blk++) {
+        uint32_t w[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            _Float16 e[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int i = 2 * j + u;
+                const float v = pr[i] > 0.0f ? pv[i] * half_at(cur.vs, i * NB + blk) : 0.0f;
+                const _Float16 hi = (_Float16)v;
+                e[u] = (_Float16)fmaf(-c.pf, (float)hi, v);
+            }
+            w[j] = (uint32_t)__builtin_bit_cast(uint16_t, e[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, e[1]) << 16);
+        }
+        const uint4 pw = c.ph ? make_uint4(0u, 0u, w[0], w[1]) : make_uint4(w[0], w[1], 0u, 0u);
+        const half8 pa = __builtin_bit_cast(half8, pw);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int t = 2 * blk + h;
+            half8 vb;
+            i8x4_to_h(word(cur.v[0][t >> 2], t & 3), vb, 0);
+            i8x4_to_h(word(cur.v[1][t >> 2], t & 3), vb, 4);
+            st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, st.acc[t], 0, 0, 0);
+        }
+    }
+}
+
+// One wave's chunk: flash attention of the group's q-heads over `ch` pages;
+// leaves O (unnormalised, true scale), m and l of each head in `slot`
+// ([kGT][D + 2] floats of LDS).
+template <int D>
+__device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, int b, int kvh, int h_base,
+                                           int gcount, int chunk, int lane, float *slot) {
+    constexpr int NB = D / 32;  // Q8_0 blocks per head row
+    constexpr int ND = D / 16;  // 16-wide d tiles of O
+    const int kg = lane >> 4;   // lane group: MFMA k-slots kg*8 .. kg*8+7
+    const int lc = lane & 15;   // S column / P' row / O column of the lane
+    const int pg0 = r.fp + chunk * p.ch;
+    const int npg = min(p.ch, r.fp + r.n_pages - pg0);
+    const int nsteps = (npg + 1) >> 1;
+
+    // physical page of chunk page `lane` (clamped into the pool by map_page)
+    const int pid_l = (int)map_page(p.pm, b, pg0 + min(lane, npg - 1));
+    const uint8_t *head_base = p.base + (int64_t)kvh * p.head_stride;
+
+    // ---- Q as the B operand of S = K.Q ----
+    const int gq = (lc >> 1) & 3;  // head of this lane's column / row
+    const int piece = lc & 1;
+    const int ph = (lc >> 3) & 1;  // page (within a step) of this lane's P' row
+    const bool qvalid = gq < gcount;
+    float qx[NB][8];
+    float qmax = 0.0f;
+    {
+        const float *qp = p.q + ((int64_t)b * p.n_heads + h_base + (qvalid ? gq : 0)) * D;
+#pragma unroll
+        for (int blk = 0; blk < NB; blk++) {
+            const float4 a = *reinterpret_cast<const float4 *>(qp + blk * 32 + kg * 8);
+            const float4 c = *reinterpret_cast<const float4 *>(qp + blk * 32 + kg * 8 + 4);
+            const float t[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const float x = qvalid ? t[s] * p.q_mul : 0.0f;
+                qx[blk][s] = x;
+                qmax = fmaxf(qmax, fabsf(x));
+            }
+        }
+    }
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+    const int qe = pow2_exp(qmax);
+    const float qs = ldexpf(1.0f, 14 - qe);
+    const float inv_qs = ldexpf(1.0f, qe - 14);
+    half8 qb[NB];
+#pragma unroll
+    for (int blk = 0; blk < NB; blk++)
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const float x = qx[blk][s] * qs;
+            const _Float16 hi = (_Float16)x;
+            const _Float16 lo = (_Float16)(x - (float)hi);
+            qb[blk][s] = piece ? lo : hi;
+        }
+
+    // ---- largest V scale of the chunk: P' = p * vscale * 2^kv stays below 2^14 ----
+    float vsc, inv_vsc;
+    {
+        float vmax = 0.0f;
+        const int units = npg * 2 * NB;  // 16-byte units of the chunk's V scales
+        for (int u0 = 0; u0 < units; u0 += 64) {
+            const int u = u0 + lane;
+            const int uu = min(u, units - 1);
+            const int pid = __shfl(pid_l, uu / (2 * NB));
+            if (u < units) {
+                const uint4 w = *reinterpret_cast<const uint4 *>(head_base + (int64_t)pid * p.page_stride + 33 * D +
+                                                                 (uu % (2 * NB)) * 16);
+                const uint4 a[1] = {w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) vmax = fmaxf(vmax, fabsf(half_at(a, i)));
+            }
+        }
+        vmax = wave_max(vmax);
+        const int ve = pow2_exp(vmax);
+        vsc = ldexpf(1.0f, 14 - ve);
+        inv_vsc = ldexpf(1.0f, ve - 14);
+    }
+
+    StepConst<D> c;
+#pragma unroll
+    for (int blk = 0; blk < NB; blk++) c.qb[blk] = qb[blk];
+    c.inv_qs = inv_qs;
+    c.vsc = vsc;
+    c.cap = p.softcap > 0.0f;
+    c.softcap = p.softcap;
+    c.inv_cap = c.cap ? 1.0f / p.softcap : 0.0f;
+    c.pg0 = pg0;
+    c.npg = npg;
+    c.start = r.start;
+    c.end = r.end;
+    c.kg = kg;
+    c.ph = ph;
+    c.pf = (float)piece;
+
+    StepState<D> st;
+#pragma unroll
+    for (int t = 0; t < ND; t++) st.acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    st.m = -INFINITY;
+    st.lsum = 0.0f;
+
+    // Two register buffers in turn: the next step's loads are in flight while
+    // this step computes (the last step reloads itself: a cache hit).
+    Raw<D> ra, rb;
+    load_step<D>(p, head_base, pid_l, 0, npg, lane, ra);
+    for (int step = 0;;) {
+        load_step<D>(p, head_base, pid_l, min(step + 1, nsteps - 1), npg, lane, rb);
+        step_body<D>(ra, step, c, st);
+        if (++step >= nsteps) break;
+        load_step<D>(p, head_base, pid_l, min(step + 1, nsteps - 1), npg, lane, ra);
+        step_body<D>(rb, step, c, st);
+        if (++step >= nsteps) break;
+    }
+    floatx4 *acc = st.acc;
+    const float m = st.m;
+    const float lsum = st.lsum;
+
+    // ---- per-head totals ----
+    // l of head gq: add the two pages (lane ^ 8) and the four lane groups
+    float L = lsum + __shfl_xor(lsum, 8);
+    L += __shfl_xor(L, 16);
+    L += __shfl_xor(L, 32);
+    // O of heads gA = 2*(kg&1), gB = gA + 1 in lanes kg = 0, 1: add pieces
+    // (row pairs) and the page-1 rows held by lane group kg + 2
+    const int gA = (2 * kg) & 3;
+    const int gB = gA + 1;
+    float oA[ND], oB[ND];
+#pragma unroll
+    for (int t = 0; t < ND; t++) {
+        oA[t] = acc[t][0] + acc[t][1];
+        oB[t] = acc[t][2] + acc[t][3];
+        oA[t] += __shfl_xor(oA[t], 32);
+        oB[t] += __shfl_xor(oB[t], 32);
+    }
+    const float LA = __shfl(L, gA * 2), LB = __shfl(L, gB * 2);
+    const float mA = __shfl(m, gA * 2), mB = __shfl(m, gB * 2);
+
+    if (lane < 32) {
+#pragma unroll
+        for (int t = 0; t < ND; t++) {
+            slot[gA * (D + 2) + t * 16 + lc] = oA[t] * inv_vsc;
+            slot[gB * (D + 2) + t * 16 + lc] = oB[t] * inv_vsc;
+        }
+        if (lc == 0) {
+            slot[gA * (D + 2) + D] = mA;
+            slot[gA * (D + 2) + D + 1] = LA;
+            slot[gB * (D + 2) + D] = mB;
+            slot[gB * (D + 2) + D + 1] = LB;
+        }
+    }
+}
+
+// Grid (workgroup split, KV head x head group, sequence); the 4 waves of a
+// workgroup take 4 consecutive chunks of the unit and merge them in LDS. A
+// unit longer than one workgroup writes one partial per workgroup.
+template <int D>
+__global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Params p) {
+    __shared__ float lds[kWaves][kGT][D + 2];
+    constexpr int kThreads = kWaves * 64;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int b = blockIdx.z;
+    const int kvh = blockIdx.y / p.n_hg;
+    const int hg = blockIdx.y - kvh * p.n_hg;
+    const int g0 = hg * kGT;
+    const int gcount = min(kGT, p.group - g0);
+    const int h_base = kvh * p.group + g0;
+    float *out = p.out + ((int64_t)b * p.n_heads + h_base) * D;
+
+    const Range r = seq_range(p, b);
+    if (r.n_pages == 0) {  // empty window: zero output (the reference's pre-zeroed buffer)
+        if (blockIdx.x == 0)
+            for (int idx = tid; idx < gcount * D; idx += kThreads) out[idx] = 0.0f;
+        return;
+    }
+    const int n_chunks = (r.n_pages + p.ch - 1) / p.ch;
+    const int n_wg = (n_chunks + kWaves - 1) / kWaves;
+    const int wg = blockIdx.x;
+    if (wg >= n_wg) return;
+    const int chunk = wg * kWaves + wave;
+    if (chunk < n_chunks) {
+        wave_chunk<D>(p, r, b, kvh, h_base, gcount, chunk, lane, &lds[wave][0][0]);
+    } else if (lane < kGT) {
+        lds[wave][lane][D] = -INFINITY;
+        lds[wave][lane][D + 1] = 0.0f;
+    }
+    __syncthreads();
+
+    // merge the workgroup's waves; thread -> (head g, element d)
+    const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
+    const int64_t pstride = (int64_t)kGT * (D + 2);  // floats per (unit, workgroup) partial
+    float *mine = p.part + (unit * p.max_wg + wg) * pstride;
+    for (int idx = tid; idx < kGT * D; idx += kThreads) {
+        const int g = idx / D;
+        const int d = idx - g * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, lds[w][g][D]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            const float mw = lds[w][g][D];
+            if (mw != -INFINITY) {
+                const float f = fast_exp2(mw - M);
+                L = fmaf(lds[w][g][D + 1], f, L);
+                A = fmaf(lds[w][g][d], f, A);
+            }
+        }
+        if (n_wg == 1) {
+            if (g < gcount) out[g * D + d] = L > 0.0f ? A * (1.0f / L) : 0.0f;
+        } else {
+            mine[g * (D + 2) + d] = A;
+            if (d == 0) {
+                mine[g * (D + 2) + D] = M;
+                mine[g * (D + 2) + D + 1] = L;
+            }
+        }
+    }
+    // Units with more than one workgroup are merged by decode_q8_combine_kernel.
+    // (Merging here in the last workgroup to finish needs a device-scope
+    // release per workgroup; on gfx950 that is an L2 writeback each time and
+    // measured ~6x slower than the extra launch.)
+}
+
+// Merge of the workgroup partials of every unit with more than one
+// workgroup; grid (kGT*D/256, KV head x head group, sequence).
+template <int D>
+__global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p) {
+    const int b = blockIdx.z;
+    const int kvh = blockIdx.y / p.n_hg;
+    const int hg = blockIdx.y - kvh * p.n_hg;
+    const int g0 = hg * kGT;
+    const int gcount = min(kGT, p.group - g0);
+    const int h_base = kvh * p.group + g0;
+    const Range r = seq_range(p, b);
+    const int n_chunks = (r.n_pages + p.ch - 1) / p.ch;
+    const int n_wg = (n_chunks + kWaves - 1) / kWaves;
+    if (n_wg <= 1) return;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    const int g = idx / D;
+    const int d = idx - g * D;
+    if (g >= gcount) return;
+    const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
+    const int64_t pstride = (int64_t)kGT * (D + 2);
+    const float *hp = p.part + unit * p.max_wg * pstride + g * (D + 2);
+    float M = -INFINITY;
+    for (int i = 0; i < n_wg; i++) M = fmaxf(M, hp[i * pstride + D]);
+    float L = 0.0f, A = 0.0f;
+    for (int i = 0; i < n_wg; i++) {
+        const float mi = hp[i * pstride + D];
+        const float f = (mi == -INFINITY) ? 0.0f : fast_exp2(mi - M);
+        L = fmaf(hp[i * pstride + D + 1], f, L);
+        A = fmaf(hp[i * pstride + d], f, A);
+    }
+    p.out[((int64_t)b * p.n_heads + h_base + g) * D + d] = L > 0.0f ? A * (1.0f / L) : 0.0f;
+}
+
+template <int D>
+int launch_d(gla_ctx *ctx, const Q8Params &prm, dim3 grid) {
+    hipLaunchKernelGGL((decode_q8_mfma_kernel<D>), grid, dim3(kWaves * 64), 0, ctx->stream, prm);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "decode_q8_mfma_kernel launch: %s", hipGetErrorString(e));
+    if (prm.max_wg > 1) {
+        hipLaunchKernelGGL((decode_q8_combine_kernel<D>), dim3(kGT * D / 256, grid.y, grid.z), dim3(256), 0,
+                           ctx->stream, prm);
+        e = hipGetLastError();
+        if (e != hipSuccess)
+            return set_error(GLA_ERR_KERNEL, "decode_q8_combine_kernel launch: %s", hipGetErrorString(e));
+    }
+    return GLA_OK;
+}
+
+}  // namespace
+
+int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
+    const int D = d.head_dim;
+    const int group = d.n_heads / d.n_kv_heads;
+    const int n_hg = (group + kGT - 1) / kGT;
+    // pages a window can span (a start inside a page adds one)
+    const int64_t max_pages = d.max_kv_len > 0 ? (d.max_kv_len + GLA_PAGE_SIZE - 1) / GLA_PAGE_SIZE + 1 : 1;
+    const int64_t units = (int64_t)d.n_seqs * d.n_kv_heads * n_hg;
+    // Chunk size: about 16k wave-chunks over the longest sequence, preferring
+    // at most kMaxChunks chunks per unit; even and 2..64 pages (a wave holds
+    // one page id per lane).
+    int64_t ch = std::max<int64_t>(2, units * max_pages / 16384);
+    ch = std::max<int64_t>(ch, (max_pages + kMaxChunks - 1) / kMaxChunks);
+    if (const char *env = getenv("GLA_Q8_CHUNK_PAGES")) {
+        const int v = atoi(env);
+        if (v > 0) ch = v;
+    }
+    ch = std::min<int64_t>(64, (ch + 1) & ~int64_t(1));
+    const int64_t max_chunks = (max_pages + ch - 1) / ch;
+
+    Q8Params prm;
+    prm.base = d.kv.k;
+    prm.page_stride = d.kv.page_stride;
+    prm.head_stride = d.kv.head_stride;
+    prm.pm = d.pm;
+    prm.kv_start = d.kv_start;
+    prm.kv_len = d.kv_len;
+    prm.q = d.q;
+    prm.out = d.out;
+    prm.n_heads = d.n_heads;
+    prm.n_kv_heads = d.n_kv_heads;
+    prm.group = group;
+    prm.n_hg = n_hg;
+    prm.ch = (int)ch;
+    const int64_t max_wg = (max_chunks + kWaves - 1) / kWaves;
+    prm.max_wg = (int)max_wg;
+    prm.max_len = d.max_kv_len;
+    const bool cap = d.softcap > 0.0f;
+    prm.q_mul = cap ? d.scale : d.scale * kLog2e;
+    prm.softcap = cap ? d.softcap : 0.0f;
+    prm.part = nullptr;
+    if (max_wg > 1) {
+        const size_t bytes = (size_t)units * max_wg * kGT * (D + 2) * sizeof(float);
+        int rc = ensure_scratch(ctx, bytes);
+        if (rc != GLA_OK) return rc;
+        prm.part = (float *)ctx->scratch;
+    }
+    if (d.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "decode: n_seqs %d > 65535", d.n_seqs);
+    dim3 grid((unsigned)max_wg, d.n_kv_heads * n_hg, d.n_seqs);
+    switch (D) {
+    case 64:
+        return launch_d<64>(ctx, prm, grid);
+    case 128:
+        return launch_d<128>(ctx, prm, grid);
+    case 256:
+        return launch_d<256>(ctx, prm, grid);
+    }
+    return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
+}
+
+}  // namespace gla

@@ -11,9 +11,19 @@
 //   Q8_0: [page][kv_head] { Kq[16][d] i8 | Vq[16][d] i8 |
 //                           Ks[16][d/32] f16 | Vs[16][d/32] f16 }    34*d B per head
 //
-// The Q8_0 split of quants and scales keeps every quant row 16-byte aligned
-// (Glint's 34-byte block, src/cache/mod.rs:276, is not); the byte count per
-// position is unchanged (34 per 32 elements) and export re-packs the blocks.
+// The Q8_0 split of quants and scales keeps every quant access 16-byte
+// aligned (Glint's 34-byte block, src/cache/mod.rs:276, is not); the byte
+// count per position is unchanged (34 per 32 elements) and export re-packs
+// the blocks.
+//
+// Q8_0 quants are stored in the order the MFMA decode kernel consumes them
+// (q8k_off / q8v_off below): lane l of a wave reads bytes [l*D/4, (l+1)*D/4)
+// of a (page, head) K or V block and gets exactly its MFMA operand bytes.
+//   K[slot t][d]: lane (kg = (d>>3)&3)*16 + t holds, for each 32-block
+//                 blk = d>>5, the 8 bytes d = blk*32 + kg*8 + 0..7.
+//   V[slot s][d]: lane (s>>2)*16 + (d&15) holds, for each 16-wide d tile
+//                 dt = d>>4, the 4 bytes of slots (s & ~3) + 0..3.
+// Scales stay row-major: Ks[slot][blk], Vs[slot][blk] f16.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -67,6 +77,17 @@ struct PageMap {
     int32_t pos_limit;
     int32_t n_slots;
 };
+
+// Byte offset of quant K[slot][d] / V[slot][d] inside a (page, head) Q8_0
+// quant block of head_dim D (16*D bytes).
+__host__ __device__ __forceinline__ int q8k_off(int slot, int d, int D) {
+    const int nb = D >> 5;
+    return ((((d >> 3) & 3) * 16 + slot) * nb + (d >> 5)) * 8 + (d & 7);
+}
+__host__ __device__ __forceinline__ int q8v_off(int slot, int d, int D) {
+    const int nd = D >> 4;
+    return (((slot >> 2) * 16 + (d & 15)) * nd + (d >> 4)) * 4 + (slot & 3);
+}
 
 __device__ __forceinline__ int64_t map_page(const PageMap &pm, int b, int lp) {
     int64_t id;
@@ -140,6 +161,7 @@ struct DecodeLaunch {
     float *out;
 };
 int launch_decode(gla_ctx *ctx, const DecodeLaunch &d);
+int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d);
 
 struct PrefillLaunch {
     KvLayout kv;

@@ -49,6 +49,17 @@ __device__ __forceinline__ int64_t scale_off(const RowOps &o, int64_t row, int g
            (int64_t)(e >> 5) * 2;
 }
 
+// Byte offset of Q8_0 quant (row, element gi) of K (which = 0) or V (1); the
+// quants of a (page, head) are stored in MFMA operand order (q8k_off / q8v_off).
+__device__ __forceinline__ int64_t q8_off(const RowOps &o, int64_t row, int gi, int which) {
+    const int64_t page = row >> 4;
+    const int slot = (int)(row & 15);
+    const int h = gi / o.head_dim;
+    const int e = gi - h * o.head_dim;
+    const int in_head = which ? q8v_off(slot, e, o.head_dim) : q8k_off(slot, e, o.head_dim);
+    return page * o.L.page_stride + (int64_t)h * o.L.head_stride + in_head;
+}
+
 __device__ __forceinline__ int8_t quantize_one(float x, float inv_d) {
     float r = roundf(x * inv_d);
     if (r < -127.0f) r = -127.0f;
@@ -99,9 +110,14 @@ __global__ __launch_bounds__(64) void write_rows_kernel(const RowOps o, const in
                 uint32_t b3 = (uint8_t)quantize_one(x[4 * j + 3], inv_d);
                 w[j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
             }
-            uint4 *qd = reinterpret_cast<uint4 *>(dst + elem_off(o, row, gi0, 1));
-            qd[0] = make_uint4(w[0], w[1], w[2], w[3]);
-            qd[1] = make_uint4(w[4], w[5], w[6], w[7]);
+            if (!which) {  // K: four 8-byte runs (d = gi0 + 8*kg .. +7)
+#pragma unroll
+                for (int kg = 0; kg < 4; kg++)
+                    *reinterpret_cast<uint2 *>(dst + q8_off(o, row, gi0 + 8 * kg, 0)) = make_uint2(w[2 * kg], w[2 * kg + 1]);
+            } else {  // V: one byte per element, 4-position columns
+#pragma unroll
+                for (int j = 0; j < 32; j++) dst[q8_off(o, row, gi0 + j, 1)] = (uint8_t)(w[j >> 2] >> ((j & 3) * 8));
+            }
             uint8_t *sb = const_cast<uint8_t *>(which ? o.L.vs : o.L.ks);
             *reinterpret_cast<uint16_t *>(sb + scale_off(o, row, gi0)) = __half_as_ushort(__float2half_rn(dsc));
         }
@@ -126,12 +142,11 @@ __global__ __launch_bounds__(64) void export_rows_kernel(const RowOps o, const i
             const uint8_t *s = src + elem_off(o, row, gi0, 4);
             for (int j = 0; j < 128; j++) out[(int64_t)gi0 * 4 + j] = s[j];
         } else {
-            const uint8_t *s = src + elem_off(o, row, gi0, 1);
             const uint8_t *sc = (which ? o.L.vs : o.L.ks) + scale_off(o, row, gi0);
             uint8_t *ob = out + (int64_t)blk * 34;
             ob[0] = sc[0];
             ob[1] = sc[1];
-            for (int j = 0; j < 32; j++) ob[2 + j] = s[j];
+            for (int j = 0; j < 32; j++) ob[2 + j] = src[q8_off(o, row, gi0 + j, which)];
         }
     }
 }
@@ -153,12 +168,11 @@ __global__ __launch_bounds__(64) void import_rows_kernel(const RowOps o, const i
             uint8_t *d = dst + elem_off(o, row, gi0, 4);
             for (int j = 0; j < 128; j++) d[j] = in[(int64_t)gi0 * 4 + j];
         } else {
-            uint8_t *d = dst + elem_off(o, row, gi0, 1);
             uint8_t *sc = const_cast<uint8_t *>(which ? o.L.vs : o.L.ks) + scale_off(o, row, gi0);
             const uint8_t *ib = in + (int64_t)blk * 34;
             sc[0] = ib[0];
             sc[1] = ib[1];
-            for (int j = 0; j < 32; j++) d[j] = ib[2 + j];
+            for (int j = 0; j < 32; j++) dst[q8_off(o, row, gi0 + j, which)] = ib[2 + j];
         }
     }
 }

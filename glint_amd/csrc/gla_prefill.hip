@@ -78,8 +78,16 @@ __device__ __forceinline__ void load_tile(const PrefillParams &p, int b, int kvh
             const int slot = kp & 15;
             const int64_t base = pid * p.kv.page_stride + head_off + (int64_t)slot * p.kv.row_stride;
             if constexpr (Q8) {
-                const uint4 kq = *reinterpret_cast<const uint4 *>(p.kv.k + base + c16 * 16);
-                const uint4 vq = *reinterpret_cast<const uint4 *>(p.kv.v + base + c16 * 16);
+                // quants in the decode kernel's MFMA operand order (gla_internal.h)
+                const int64_t hb = pid * p.kv.page_stride + head_off;
+                const uint2 ka = *reinterpret_cast<const uint2 *>(p.kv.k + hb + q8k_off(slot, c16 * 16, D));
+                const uint2 kb = *reinterpret_cast<const uint2 *>(p.kv.k + hb + q8k_off(slot, c16 * 16 + 8, D));
+                const uint4 kq = make_uint4(ka.x, ka.y, kb.x, kb.y);
+                uint32_t vw4[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    vw4[e >> 2] |= (uint32_t)p.kv.v[hb + q8v_off(slot, c16 * 16 + e, D)] << ((e & 3) * 8);
+                const uint4 vq = make_uint4(vw4[0], vw4[1], vw4[2], vw4[3]);
                 const int64_t sb = pid * p.kv.page_stride + head_off + (int64_t)slot * p.kv.srow_stride +
                                    ((c16 * 16) >> 5) * 2;
                 const float ksc = __half2float(__ushort_as_half(*reinterpret_cast<const uint16_t *>(p.kv.ks + sb)));
