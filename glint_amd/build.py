@@ -36,6 +36,9 @@ HIP_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the decode kernel rescales them on the VALU,
+    # which otherwise costs an AGPR->VGPR->AGPR round trip per step
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{ROOT / 'include'}",
 ]
 HIP_SOURCES = ["gla_capi.hip", "gla_kvstore.hip", "gla_decode.hip", "gla_decode_q8.hip", "gla_prefill.hip"]

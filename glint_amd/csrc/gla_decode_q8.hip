@@ -15,25 +15,28 @@
 //
 // Exactness. int8 values are exact in f16. q and the probabilities are f32;
 // each is split into two f16 pieces (hi = f16(x), lo = f16(x - hi)) after a
-// power-of-two rescale that puts the largest magnitude in [2^13, 2^14), so
+// power-of-two rescale that puts the largest magnitude below 2^14, so
 // hi + lo carries ~22 significant bits and no piece is subnormal where it
 // matters. The MFMA multiplies f16 pairs exactly and accumulates in f32.
 //
 // Work: one wave = one (sequence, KV head, group of <= 4 q-heads, chunk of
-// `ch` pages); a workgroup is 4 independent waves. A step covers two pages
-// (32 positions), the K depth of one P.V MFMA.
+// `ch` pages); a workgroup is 4 waves on 4 consecutive chunks. A step covers
+// two pages (32 positions), the K depth of one P.V MFMA.
 //   S = K . Q   A = K tile (16 positions x one 32-element Q8_0 block), B = Q:
-//               column j = (head (j>>1)&3, piece j&1); columns 8-15 repeat 0-7.
-//               One MFMA per block per page; the block scale multiplies the
-//               per-block partial score of each position.
+//               column j = (head (j>>1)&3, piece j&1); columns 0-7 carry the
+//               even blocks and columns 8-15 the odd blocks (zero operand
+//               halves), so every lane scales only its own blocks' partial
+//               scores and one row rotation adds the two halves.
 //   O += P' . V A = P' (row r = (page r>>3 of the step, head, piece)), B = V
 //               tile (32 positions x 16 d); P'[r][t] = piece of
 //               p[t] * vscale[t][block] * 2^kv. Rows of page 0 are zero on
 //               page-1 positions and vice versa, so a lane builds only the
 //               values of its own page and every lane's S column is exactly
 //               its P' row: no data moves between lanes.
-// The Q8_0 quants are stored in this operand order (gla_internal.h), so each
-// lane's operands for a page are one contiguous D/4-byte span.
+// Quants are stored sign-flipped (x + 128) in this operand order
+// (gla_internal.h), so each lane's operands for a page are one contiguous
+// D/4-byte span and a byte becomes an exact f16 with one permute and one
+// packed subtract per two elements.
 // The 4 waves of a workgroup merge their chunks (log-sum-exp) in LDS; units
 // longer than a workgroup are merged by a second, small kernel.
 #include <math.h>
@@ -49,12 +52,13 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kGT = 4;  // q-heads per wave
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kMaxChunks = 64;  // preferred bound on chunks per unit (one merge pass)
+constexpr int kMaxChunks = 64;  // preferred bound on chunks per unit
 
 struct Q8Params {
     const uint8_t *base;  // KV storage; a (page, head) block is 34*D bytes
@@ -65,12 +69,12 @@ struct Q8Params {
     const int32_t *kv_len;
     const float *q;
     float *out;
-    float *part;   // [unit][max_wg][kGT][D + 2]: O (unnormalised), m, l
+    float *part;  // [unit][max_wg][kGT][D + 2]: O (unnormalised), m, l
     int n_heads;
     int n_kv_heads;
     int group;
     int n_hg;
-    int ch;  // pages per chunk (even)
+    int ch;      // pages per chunk (even)
     int max_wg;  // workgroups per unit (partials per unit)
     int max_len;
     float q_mul;    // scale*log2(e), or scale with a soft-cap
@@ -113,18 +117,12 @@ __device__ __forceinline__ float tanh_approx(float x) {
     return copysignf((1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t), x);
 }
 
-// Two int8 (selected from xb = bytes ^ 0x80 by `sel`) -> two exact f16:
-// 0x64XX is 1024 + XX in f16, and XX = x + 128.
-__device__ __forceinline__ half2v i8x2_to_h2(uint32_t xb, uint32_t sel) {
-    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, xb, sel);
-    return __builtin_bit_cast(half2v, h) - (half2v){(_Float16)1152.0f, (_Float16)1152.0f};
-}
-
-// Four int8 of a dword, in byte order, as halves 0..3 of `o` starting at `at`.
-__device__ __forceinline__ void i8x4_to_h(uint32_t w, half8 &o, int at) {
-    const uint32_t x = w ^ 0x80808080u;
-    const half2v a = i8x2_to_h2(x, 0x04010400u);
-    const half2v c = i8x2_to_h2(x, 0x04030402u);
+// Four stored quants (x + 128, in byte order) -> halves at..at+3 of `o`:
+// 0x64XX is 1024 + XX in f16, so subtracting 1152 leaves x exactly.
+__device__ __forceinline__ void q4_to_h(uint32_t u, half8 &o, int at) {
+    const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const half2v a = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
+    const half2v c = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
     o[at + 0] = a[0];
     o[at + 1] = a[1];
     o[at + 2] = c[0];
@@ -135,16 +133,38 @@ __device__ __forceinline__ uint32_t word(const uint4 &v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
-// f16 number `i` of a packed array of uint4.
+// f16 number i of a packed word array.
 template <int N>
-__device__ __forceinline__ float half_at(const uint4 (&a)[N], int i) {
-    const uint32_t w = word(a[i >> 3], (i >> 1) & 3);
-    const uint16_t h = (i & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffff);
-    return (float)__builtin_bit_cast(_Float16, h);
+__device__ __forceinline__ float half_at(const uint32_t (&a)[N], int i) {
+    const uint32_t w = a[i >> 1];
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)((i & 1) ? (w >> 16) : (w & 0xffff)));
 }
 
 __device__ __forceinline__ float dpp_swap1(float x) {  // lane ^ 1
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float dpp_ror8(float x) {  // lane ^ 8 within a row of 16
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
+}
+
+// Across the four rows of 16 lanes (lane ^ 16, lane ^ 32) with the gfx950
+// row swaps: VALU only, no LDS round trip.
+__device__ __forceinline__ float max_rows(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+__device__ __forceinline__ float sum_rows(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
+__device__ __forceinline__ float sum_halves(float x) {  // lane ^ 32
+    const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(c[0]) + __uint_as_float(c[1]);
 }
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -153,54 +173,149 @@ __device__ __forceinline__ float wave_max(float x) {
     return x;
 }
 
-// 2^(14 - e) where x = m * 2^e, m in [0.5, 1): maps max|.| into [2^13, 2^14).
+// e with x = m * 2^e, m in [0.5, 1); scaling by 2^(14 - e) maps max|.| below 2^14.
 __device__ __forceinline__ int pow2_exp(float x) {
     int e = 0;
     (void)frexpf(x, &e);
     return e < -100 ? -100 : (e > 100 ? 100 : e);
 }
 
+// The lane's operands of one step, in registers.
 template <int D>
 struct Raw {
-    static constexpr int NV = D / 64;  // uint4 per lane per (page, head) K or V block
-    static constexpr int NS = D / 64;  // uint4 per lane of 4 positions' scales (4 * D/32 f16)
-    uint4 k[2][NV];
-    uint4 v[2][NV];
-    uint4 ks[2][NS];
-    uint4 vs[NS];  // the lane's P.V page only
+    static constexpr int NQ = D / 64;  // uint4 per lane per (page, head) K or V block
+    static constexpr int NB = D / 32;
+    uint4 k[2][NQ];
+    uint4 v[2][NQ];
+    uint32_t ks[2][NB];   // 4 positions x the lane's NB/2 blocks, per page
+    uint32_t vs[2 * NB];  // 4 positions x NB blocks, the lane's P.V page only
 };
 
+// ---- the LDS slot: direct global -> LDS loads (gfx950 global_load_lds) ----
+//
+// Each wave streams its chunk through one LDS slot of two pages:
+// K_a | K_b | V_a | V_b (16*D bytes each, byte copies of the (page, head)
+// quant blocks) and the scales Ks_a | Ks_b | Vs_a | Vs_b (D bytes each). At
+// the top of a step the wave copies the slot into registers and refills it
+// with the next step, which is then in flight while this step computes.
+// The loads are issued from inline assembly with explicit vmcnt waits: the
+// compiler's own wait insertion would wait for every outstanding LDS load
+// before any LDS read. Every vector-memory instruction of the streaming loop
+// is one of these, so the counts are exact; the compiler's waits for its own
+// earlier loads stay correct because extra outstanding loads only make an
+// in-order wait wait longer.
+constexpr int kSlotBytesPerD = 68;  // 64*D quant bytes + 4*D scale bytes per step
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// 16 bytes per lane from g into LDS at m0 + 16*lane (m0 restored afterwards).
+__device__ __forceinline__ void dma16(const void *g, uint32_t m0) {
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(g), "s"(m0)
+        : "memory");
+}
+
+// 4 bytes per lane from g into LDS at m0 + 4*lane.
+__device__ __forceinline__ void dma4(const void *g, uint32_t m0) {
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dword %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(g), "s"(m0)
+        : "memory");
+}
+
+__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Issue the loads of step `step` (pages 2*step, 2*step+1 of the chunk) into
+// the slot at LDS byte address `slot`.
 template <int D>
-__device__ __forceinline__ void load_step(const Q8Params &p, const uint8_t *head_base, int pid_l, int step,
-                                          int npg, int lane, Raw<D> &r) {
-    constexpr int LB = D / 4;  // quant bytes per lane per page
+__device__ __forceinline__ void issue_step(const Q8Params &p, const uint8_t *head_base, int pid_l, int step,
+                                           int npg, int lane, uint32_t slot) {
+    constexpr int NQ = D / 64;
     const int pa = 2 * step;
     const int pb = (pa + 1 < npg) ? pa + 1 : pa;
     const int ida = __builtin_amdgcn_readlane(pid_l, pa);
     const int idb = __builtin_amdgcn_readlane(pid_l, pb);
     const uint8_t *ba = head_base + (int64_t)ida * p.page_stride;
     const uint8_t *bb = head_base + (int64_t)idb * p.page_stride;
+    // lane l's operand bytes [l*D/4, (l+1)*D/4) land as NQ pieces 1 KB apart
+#pragma unroll
+    for (int c = 0; c < NQ; c++) {
+        dma16(ba + lane * (D / 4) + c * 16, slot + 0 * 16 * D + c * 1024);
+        dma16(bb + lane * (D / 4) + c * 16, slot + 1 * 16 * D + c * 1024);
+        dma16(ba + 16 * D + lane * (D / 4) + c * 16, slot + 2 * 16 * D + c * 1024);
+        dma16(bb + 16 * D + lane * (D / 4) + c * 16, slot + 3 * 16 * D + c * 1024);
+    }
+    // scales, byte-identical: [Ks_a | Ks_b | Vs_a | Vs_b], 256 bytes per load
+#pragma unroll
+    for (int j = 0; j < D / 64; j++) {
+        const int i = j * 256 + lane * 4;
+        const int reg = i / D;  // 0 Ks_a, 1 Ks_b, 2 Vs_a, 3 Vs_b
+        const uint8_t *src = ((reg & 1) ? bb : ba) + (reg < 2 ? 32 * D : 33 * D) + (i - reg * D);
+        dma4(src, slot + 64 * D + j * 256);
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void lds_words(const uint8_t *src, uint32_t (&dst)[N]) {
+    static_assert(N % 2 == 0, "whole 8-byte reads");
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 4; i++) {
+            const uint4 w = reinterpret_cast<const uint4 *>(src)[i];
+            dst[4 * i] = w.x;
+            dst[4 * i + 1] = w.y;
+            dst[4 * i + 2] = w.z;
+            dst[4 * i + 3] = w.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 2; i++) {
+            const uint2 w = reinterpret_cast<const uint2 *>(src)[i];
+            dst[2 * i] = w.x;
+            dst[2 * i + 1] = w.y;
+        }
+    }
+}
+
+// Copy the lane's operands of a landed step from the slot.
+template <int D>
+__device__ __forceinline__ void read_step(const uint8_t *slot, int lane, Raw<D> &r) {
+    constexpr int NQ = D / 64;
+    constexpr int NB = D / 32;
     const int kg = lane >> 4;
-    const int ph = (lane >> 3) & 1;
+    const int hb = (lane >> 3) & 1;  // the lane's block parity (S) / page (P'.V)
 #pragma unroll
-    for (int i = 0; i < Raw<D>::NV; i++) {
-        r.k[0][i] = reinterpret_cast<const uint4 *>(ba + lane * LB)[i];
-        r.k[1][i] = reinterpret_cast<const uint4 *>(bb + lane * LB)[i];
-        r.v[0][i] = reinterpret_cast<const uint4 *>(ba + 16 * D + lane * LB)[i];
-        r.v[1][i] = reinterpret_cast<const uint4 *>(bb + 16 * D + lane * LB)[i];
+    for (int c = 0; c < NQ; c++) {
+        r.k[0][c] = *reinterpret_cast<const uint4 *>(slot + 0 * 16 * D + c * 1024 + lane * 16);
+        r.k[1][c] = *reinterpret_cast<const uint4 *>(slot + 1 * 16 * D + c * 1024 + lane * 16);
+        r.v[0][c] = *reinterpret_cast<const uint4 *>(slot + 2 * 16 * D + c * 1024 + lane * 16);
+        r.v[1][c] = *reinterpret_cast<const uint4 *>(slot + 3 * 16 * D + c * 1024 + lane * 16);
     }
-    const int soff = kg * 4 * (D / 32) * 2;  // first of the lane's 4 positions
-#pragma unroll
-    for (int i = 0; i < Raw<D>::NS; i++) {
-        r.ks[0][i] = reinterpret_cast<const uint4 *>(ba + 32 * D + soff)[i];
-        r.ks[1][i] = reinterpret_cast<const uint4 *>(bb + 32 * D + soff)[i];
-        r.vs[i] = reinterpret_cast<const uint4 *>((ph ? bb : ba) + 33 * D + soff)[i];
-    }
+    // K scales: [parity][slot][NB/2] f16; the lane's 4 positions of its parity
+    const uint8_t *ks = slot + 64 * D + (hb * 16 + kg * 4) * NB;
+    lds_words(ks, r.ks[0]);
+    lds_words(ks + D, r.ks[1]);
+    // V scales: [slot][NB] f16; the lane's 4 positions of its page
+    lds_words(slot + 64 * D + (2 + hb) * D + kg * 4 * NB * 2, r.vs);
 }
 
 template <int D>
 struct StepConst {
-    half8 qb[D / 32];
+    half8 qb[D / 32];  // Q operand per block (zero unless the block's parity is the lane's)
     float inv_qs, vsc, softcap, inv_cap;
     bool cap;
     int pg0, npg, start, end;
@@ -217,7 +332,7 @@ struct StepState {
 
 // One step: two pages (32 positions) of one (sequence, KV head).
 template <int D>
-__device__ __forceinline__ void step_body(const Raw<D> &cur, int step, const StepConst<D> &c, StepState<D> &st) {
+__device__ __forceinline__ void step_body(Raw<D> &cur, int step, const StepConst<D> &c, StepState<D> &st) {
     constexpr int NB = D / 32;
     constexpr int ND = D / 16;
 
@@ -225,20 +340,23 @@ __device__ __forceinline__ void step_body(const Raw<D> &cur, int step, const Ste
     float s0[4], s1[4];
 #pragma unroll
     for (int P = 0; P < 2; P++) {
-        floatx4 cb[NB];
+        floatx4 cp[NB / 2];
+#pragma unroll
+        for (int j = 0; j < NB / 2; j++) cp[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int blk = 0; blk < NB; blk++) {
             half8 a;
-            i8x4_to_h(word(cur.k[P][blk >> 1], (blk & 1) * 2), a, 0);
-            i8x4_to_h(word(cur.k[P][blk >> 1], (blk & 1) * 2 + 1), a, 4);
-            cb[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, c.qb[blk], floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            q4_to_h(word(cur.k[P][blk >> 1], (blk & 1) * 2), a, 0);
+            q4_to_h(word(cur.k[P][blk >> 1], (blk & 1) * 2 + 1), a, 4);
+            cp[blk >> 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, c.qb[blk], cp[blk >> 1], 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             float x = 0.0f;
 #pragma unroll
-            for (int blk = 0; blk < NB; blk++) x = fmaf(half_at(cur.ks[P], i * NB + blk), cb[blk][i], x);
+            for (int j = 0; j < NB / 2; j++) x = fmaf(half_at(cur.ks[P], i * (NB / 2) + j), cp[j][i], x);
             x *= c.inv_qs;
+            x += dpp_ror8(x);   // even blocks + odd blocks
             x += dpp_swap1(x);  // hi piece + lo piece
             if (P == 0)
                 s0[i] = x;
@@ -254,21 +372,27 @@ __device__ __forceinline__ void step_body(const Raw<D> &cur, int step, const Ste
         }
     }
 
-    // window / length mask (only a chunk's first and last steps can hold
-    // positions outside [start, end)), running max
+    // Window / length mask: only a chunk's first and last steps can hold
+    // positions outside [start, end). Masked positions get score -inf and,
+    // on the lane's own page, a zero V scale, so a non-finite scale of an
+    // unused position cannot reach the output.
     const int sp = (c.pg0 + 2 * step) * 16;             // first position of the step
     const int lim1 = min(c.end, (c.pg0 + c.npg) * 16);  // page 1 of the step may be past the chunk
-    if (sp < c.start || sp + 32 > lim1) {               // wave-uniform
+    if (sp < c.start || sp + 32 > lim1) {
         const int pos0 = sp + c.kg * 4;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            s0[i] = (pos0 + i >= c.start && pos0 + i < c.end) ? s0[i] : -INFINITY;
-            s1[i] = (pos0 + 16 + i >= c.start && pos0 + 16 + i < lim1) ? s1[i] : -INFINITY;
+            const bool ok0 = pos0 + i >= c.start && pos0 + i < c.end;
+            const bool ok1 = pos0 + 16 + i >= c.start && pos0 + 16 + i < lim1;
+            s0[i] = ok0 ? s0[i] : -INFINITY;
+            s1[i] = ok1 ? s1[i] : -INFINITY;
+            const bool ok = c.ph ? ok1 : ok0;
+#pragma unroll
+            for (int w = 0; w < NB / 2; w++) cur.vs[i * (NB / 2) + w] = ok ? cur.vs[i * (NB / 2) + w] : 0u;
         }
     }
-    float tmax = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float tmax = max_rows(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                                      fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))));
     const float m_new = fmaxf(st.m, tmax);  // finite: page 0 of a step always holds a position
     const float alpha = fast_exp2(st.m - m_new);
     st.m = m_new;
@@ -298,38 +422,34 @@ __device__ __forceinline__ void step_body(const Raw<D> &cur, int step, const Ste
     for (int i = 0; i < 4; i++) pv[i] = pr[i] * c.vsc;
 #pragma unroll
     for (int blk = 0; blk < NB; blk++) {
-        uint32_t w[2];
+        float v[4];
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            _Float16 e[2];
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int i = 2 * j + u;
-                const float v = pr[i] > 0.0f ? pv[i] * half_at(cur.vs, i * NB + blk) : 0.0f;
-                const _Float16 hi = (_Float16)v;
-                e[u] = (_Float16)fmaf(-c.pf, (float)hi, v);
-            }
-            w[j] = (uint32_t)__builtin_bit_cast(uint16_t, e[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, e[1]) << 16);
-        }
-        const uint4 pw = c.ph ? make_uint4(0u, 0u, w[0], w[1]) : make_uint4(w[0], w[1], 0u, 0u);
+        for (int i = 0; i < 4; i++) v[i] = pv[i] * half_at(cur.vs, i * NB + blk);
+        const half2v h01 = __builtin_convertvector((float2v){v[0], v[1]}, half2v);
+        const half2v h23 = __builtin_convertvector((float2v){v[2], v[3]}, half2v);
+        const half2v e01 = {(_Float16)fmaf(-c.pf, (float)h01[0], v[0]), (_Float16)fmaf(-c.pf, (float)h01[1], v[1])};
+        const half2v e23 = {(_Float16)fmaf(-c.pf, (float)h23[0], v[2]), (_Float16)fmaf(-c.pf, (float)h23[1], v[3])};
+        const uint32_t w0 = __builtin_bit_cast(uint32_t, e01);
+        const uint32_t w1 = __builtin_bit_cast(uint32_t, e23);
+        const uint4 pw = c.ph ? make_uint4(0u, 0u, w0, w1) : make_uint4(w0, w1, 0u, 0u);
         const half8 pa = __builtin_bit_cast(half8, pw);
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int t = 2 * blk + h;
             half8 vb;
-            i8x4_to_h(word(cur.v[0][t >> 2], t & 3), vb, 0);
-            i8x4_to_h(word(cur.v[1][t >> 2], t & 3), vb, 4);
+            q4_to_h(word(cur.v[0][t >> 2], t & 3), vb, 0);
+            q4_to_h(word(cur.v[1][t >> 2], t & 3), vb, 4);
             st.acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, st.acc[t], 0, 0, 0);
         }
     }
 }
 
 // One wave's chunk: flash attention of the group's q-heads over `ch` pages;
-// leaves O (unnormalised, true scale), m and l of each head in `slot`
-// ([kGT][D + 2] floats of LDS).
+// leaves O (unnormalised, true scale), m and l of each head at the start of
+// the wave's LDS slot ([kGT][D + 2] floats).
 template <int D>
 __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, int b, int kvh, int h_base,
-                                           int gcount, int chunk, int lane, float *slot) {
+                                           int gcount, int chunk, int lane, uint8_t *slot) {
     constexpr int NB = D / 32;  // Q8_0 blocks per head row
     constexpr int ND = D / 16;  // 16-wide d tiles of O
     const int kg = lane >> 4;   // lane group: MFMA k-slots kg*8 .. kg*8+7
@@ -342,10 +462,14 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
     const int pid_l = (int)map_page(p.pm, b, pg0 + min(lane, npg - 1));
     const uint8_t *head_base = p.base + (int64_t)kvh * p.head_stride;
 
+    // start streaming step 0; q and the V-scale scan overlap it
+    const uint32_t slot_lds = __builtin_amdgcn_readfirstlane(lds_addr(slot));
+    issue_step<D>(p, head_base, pid_l, 0, npg, lane, slot_lds);
+
     // ---- Q as the B operand of S = K.Q ----
     const int gq = (lc >> 1) & 3;  // head of this lane's column / row
     const int piece = lc & 1;
-    const int ph = (lc >> 3) & 1;  // page (within a step) of this lane's P' row
+    const int ph = (lc >> 3) & 1;  // block parity of the column; page of the P' row
     const bool qvalid = gq < gcount;
     float qx[NB][8];
     float qmax = 0.0f;
@@ -354,22 +478,20 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
 #pragma unroll
         for (int blk = 0; blk < NB; blk++) {
             const float4 a = *reinterpret_cast<const float4 *>(qp + blk * 32 + kg * 8);
-            const float4 c = *reinterpret_cast<const float4 *>(qp + blk * 32 + kg * 8 + 4);
-            const float t[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+            const float4 e = *reinterpret_cast<const float4 *>(qp + blk * 32 + kg * 8 + 4);
+            const float t[8] = {a.x, a.y, a.z, a.w, e.x, e.y, e.z, e.w};
 #pragma unroll
             for (int s = 0; s < 8; s++) {
-                const float x = qvalid ? t[s] * p.q_mul : 0.0f;
+                const float x = t[s] * p.q_mul;
                 qx[blk][s] = x;
                 qmax = fmaxf(qmax, fabsf(x));
             }
         }
     }
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+    qmax = max_rows(qmax);
     const int qe = pow2_exp(qmax);
     const float qs = ldexpf(1.0f, 14 - qe);
-    const float inv_qs = ldexpf(1.0f, qe - 14);
-    half8 qb[NB];
+    StepConst<D> c;
 #pragma unroll
     for (int blk = 0; blk < NB; blk++)
 #pragma unroll
@@ -377,11 +499,13 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
             const float x = qx[blk][s] * qs;
             const _Float16 hi = (_Float16)x;
             const _Float16 lo = (_Float16)(x - (float)hi);
-            qb[blk][s] = piece ? lo : hi;
+            const bool mine = qvalid && ((blk & 1) == ph);
+            c.qb[blk][s] = mine ? (piece ? lo : hi) : (_Float16)0.0f;
         }
+    c.inv_qs = ldexpf(1.0f, qe - 14);
 
     // ---- largest V scale of the chunk: P' = p * vscale * 2^kv stays below 2^14 ----
-    float vsc, inv_vsc;
+    float inv_vsc;
     {
         float vmax = 0.0f;
         const int units = npg * 2 * NB;  // 16-byte units of the chunk's V scales
@@ -392,22 +516,17 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
             if (u < units) {
                 const uint4 w = *reinterpret_cast<const uint4 *>(head_base + (int64_t)pid * p.page_stride + 33 * D +
                                                                  (uu % (2 * NB)) * 16);
-                const uint4 a[1] = {w};
+                const uint32_t a[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
                 for (int i = 0; i < 8; i++) vmax = fmaxf(vmax, fabsf(half_at(a, i)));
             }
         }
         vmax = wave_max(vmax);
         const int ve = pow2_exp(vmax);
-        vsc = ldexpf(1.0f, 14 - ve);
+        c.vsc = ldexpf(1.0f, 14 - ve);
         inv_vsc = ldexpf(1.0f, ve - 14);
     }
 
-    StepConst<D> c;
-#pragma unroll
-    for (int blk = 0; blk < NB; blk++) c.qb[blk] = qb[blk];
-    c.inv_qs = inv_qs;
-    c.vsc = vsc;
     c.cap = p.softcap > 0.0f;
     c.softcap = p.softcap;
     c.inv_cap = c.cap ? 1.0f / p.softcap : 0.0f;
@@ -425,27 +544,21 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
     st.m = -INFINITY;
     st.lsum = 0.0f;
 
-    // Two register buffers in turn: the next step's loads are in flight while
-    // this step computes (the last step reloads itself: a cache hit).
-    Raw<D> ra, rb;
-    load_step<D>(p, head_base, pid_l, 0, npg, lane, ra);
-    for (int step = 0;;) {
-        load_step<D>(p, head_base, pid_l, min(step + 1, nsteps - 1), npg, lane, rb);
-        step_body<D>(ra, step, c, st);
-        if (++step >= nsteps) break;
-        load_step<D>(p, head_base, pid_l, min(step + 1, nsteps - 1), npg, lane, ra);
-        step_body<D>(rb, step, c, st);
-        if (++step >= nsteps) break;
+    for (int step = 0; step < nsteps; step++) {
+        wait_vmem_all();  // step `step` has landed
+        Raw<D> cur;
+        read_step<D>(slot, lane, cur);
+        if (step + 1 < nsteps) {
+            wait_lds();  // the slot is copied: refill it with the next step
+            issue_step<D>(p, head_base, pid_l, step + 1, npg, lane, slot_lds);
+        }
+        step_body<D>(cur, step, c, st);
     }
-    floatx4 *acc = st.acc;
-    const float m = st.m;
-    const float lsum = st.lsum;
+    wait_vmem_all();
 
     // ---- per-head totals ----
     // l of head gq: add the two pages (lane ^ 8) and the four lane groups
-    float L = lsum + __shfl_xor(lsum, 8);
-    L += __shfl_xor(L, 16);
-    L += __shfl_xor(L, 32);
+    const float L = sum_rows(st.lsum + dpp_ror8(st.lsum));
     // O of heads gA = 2*(kg&1), gB = gA + 1 in lanes kg = 0, 1: add pieces
     // (row pairs) and the page-1 rows held by lane group kg + 2
     const int gA = (2 * kg) & 3;
@@ -453,25 +566,26 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
     float oA[ND], oB[ND];
 #pragma unroll
     for (int t = 0; t < ND; t++) {
-        oA[t] = acc[t][0] + acc[t][1];
-        oB[t] = acc[t][2] + acc[t][3];
-        oA[t] += __shfl_xor(oA[t], 32);
-        oB[t] += __shfl_xor(oB[t], 32);
+        oA[t] = sum_halves(st.acc[t][0] + st.acc[t][1]);
+        oB[t] = sum_halves(st.acc[t][2] + st.acc[t][3]);
     }
     const float LA = __shfl(L, gA * 2), LB = __shfl(L, gB * 2);
-    const float mA = __shfl(m, gA * 2), mB = __shfl(m, gB * 2);
+    const float mA = __shfl(st.m, gA * 2), mB = __shfl(st.m, gB * 2);
 
+    // the slot is idle now (every load has landed): it holds this wave's
+    // result for the workgroup merge
+    float *res = reinterpret_cast<float *>(slot);
     if (lane < 32) {
 #pragma unroll
         for (int t = 0; t < ND; t++) {
-            slot[gA * (D + 2) + t * 16 + lc] = oA[t] * inv_vsc;
-            slot[gB * (D + 2) + t * 16 + lc] = oB[t] * inv_vsc;
+            res[gA * (D + 2) + t * 16 + lc] = oA[t] * inv_vsc;
+            res[gB * (D + 2) + t * 16 + lc] = oB[t] * inv_vsc;
         }
         if (lc == 0) {
-            slot[gA * (D + 2) + D] = mA;
-            slot[gA * (D + 2) + D + 1] = LA;
-            slot[gB * (D + 2) + D] = mB;
-            slot[gB * (D + 2) + D + 1] = LB;
+            res[gA * (D + 2) + D] = mA;
+            res[gA * (D + 2) + D + 1] = LA;
+            res[gB * (D + 2) + D] = mB;
+            res[gB * (D + 2) + D + 1] = LB;
         }
     }
 }
@@ -481,7 +595,9 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
 // unit longer than one workgroup writes one partial per workgroup.
 template <int D>
 __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Params p) {
-    __shared__ float lds[kWaves][kGT][D + 2];
+    // per wave: the streaming slot, later the wave's [kGT][D + 2] result
+    __shared__ __attribute__((aligned(16))) uint8_t slots[kWaves][kSlotBytesPerD * D];
+    static_assert(kGT * (D + 2) * 4 <= kSlotBytesPerD * D, "the merge result fits in the slot");
     constexpr int kThreads = kWaves * 64;
 
     const int tid = threadIdx.x;
@@ -507,12 +623,16 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
     if (wg >= n_wg) return;
     const int chunk = wg * kWaves + wave;
     if (chunk < n_chunks) {
-        wave_chunk<D>(p, r, b, kvh, h_base, gcount, chunk, lane, &lds[wave][0][0]);
+        wave_chunk<D>(p, r, b, kvh, h_base, gcount, chunk, lane, slots[wave]);
     } else if (lane < kGT) {
-        lds[wave][lane][D] = -INFINITY;
-        lds[wave][lane][D + 1] = 0.0f;
+        float *res = reinterpret_cast<float *>(slots[wave]);
+        res[lane * (D + 2) + D] = -INFINITY;
+        res[lane * (D + 2) + D + 1] = 0.0f;
     }
     __syncthreads();
+    auto res = [&](int w, int g, int i) -> float {
+        return reinterpret_cast<const float *>(slots[w])[g * (D + 2) + i];
+    };
 
     // merge the workgroup's waves; thread -> (head g, element d)
     const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
@@ -523,15 +643,15 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
         const int d = idx - g * D;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) M = fmaxf(M, lds[w][g][D]);
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, res(w, g, D));
         float L = 0.0f, A = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; w++) {
-            const float mw = lds[w][g][D];
+            const float mw = res(w, g, D);
             if (mw != -INFINITY) {
                 const float f = fast_exp2(mw - M);
-                L = fmaf(lds[w][g][D + 1], f, L);
-                A = fmaf(lds[w][g][d], f, A);
+                L = fmaf(res(w, g, D + 1), f, L);
+                A = fmaf(res(w, g, d), f, A);
             }
         }
         if (n_wg == 1) {
@@ -618,6 +738,7 @@ int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
     }
     ch = std::min<int64_t>(64, (ch + 1) & ~int64_t(1));
     const int64_t max_chunks = (max_pages + ch - 1) / ch;
+    const int64_t max_wg = (max_chunks + kWaves - 1) / kWaves;
 
     Q8Params prm;
     prm.base = d.kv.k;
@@ -633,7 +754,6 @@ int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
     prm.group = group;
     prm.n_hg = n_hg;
     prm.ch = (int)ch;
-    const int64_t max_wg = (max_chunks + kWaves - 1) / kWaves;
     prm.max_wg = (int)max_wg;
     prm.max_len = d.max_kv_len;
     const bool cap = d.softcap > 0.0f;

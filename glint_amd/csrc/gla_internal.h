@@ -16,14 +16,16 @@
 // count per position is unchanged (34 per 32 elements) and export re-packs
 // the blocks.
 //
-// Q8_0 quants are stored in the order the MFMA decode kernel consumes them
-// (q8k_off / q8v_off below): lane l of a wave reads bytes [l*D/4, (l+1)*D/4)
-// of a (page, head) K or V block and gets exactly its MFMA operand bytes.
+// Q8_0 quants are stored as x + 128 (sign bit flipped; a zeroed page holds
+// 0x80 bytes) in the order the MFMA decode kernel consumes them (q8k_off /
+// q8v_off below): lane l of a wave reads bytes [l*D/4, (l+1)*D/4) of a
+// (page, head) K or V block and gets exactly its MFMA operand bytes.
 //   K[slot t][d]: lane (kg = (d>>3)&3)*16 + t holds, for each 32-block
 //                 blk = d>>5, the 8 bytes d = blk*32 + kg*8 + 0..7.
 //   V[slot s][d]: lane (s>>2)*16 + (d&15) holds, for each 16-wide d tile
 //                 dt = d>>4, the 4 bytes of slots (s & ~3) + 0..3.
-// Scales stay row-major: Ks[slot][blk], Vs[slot][blk] f16.
+// K scales are grouped by block parity, Ks[blk & 1][slot][blk >> 1]
+// (q8ks_off), V scales are row-major, Vs[slot][blk], all f16.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -87,6 +89,10 @@ __host__ __device__ __forceinline__ int q8k_off(int slot, int d, int D) {
 __host__ __device__ __forceinline__ int q8v_off(int slot, int d, int D) {
     const int nd = D >> 4;
     return (((slot >> 2) * 16 + (d & 15)) * nd + (d >> 4)) * 4 + (slot & 3);
+}
+// f16 index of the K scale of (slot, block) inside a (page, head) Ks array.
+__host__ __device__ __forceinline__ int q8ks_off(int slot, int blk, int D) {
+    return ((blk & 1) * 16 + slot) * (D >> 6) + (blk >> 1);
 }
 
 __device__ __forceinline__ int64_t map_page(const PageMap &pm, int b, int lp) {

@@ -40,13 +40,15 @@ __device__ __forceinline__ int64_t elem_off(const RowOps &o, int64_t row, int gi
     return page * o.L.page_stride + (int64_t)h * o.L.head_stride + (int64_t)slot * o.L.row_stride +
            (int64_t)e * esize;
 }
-__device__ __forceinline__ int64_t scale_off(const RowOps &o, int64_t row, int gi) {
+// Byte offset of the Q8_0 scale of (row, element gi) from L.ks (which = 0,
+// parity-grouped) or L.vs (which = 1, row-major).
+__device__ __forceinline__ int64_t scale_off(const RowOps &o, int64_t row, int gi, int which) {
     const int64_t page = row >> 4;
     const int slot = (int)(row & 15);
     const int h = gi / o.head_dim;
     const int e = gi - h * o.head_dim;
-    return page * o.L.page_stride + (int64_t)h * o.L.head_stride + (int64_t)slot * o.L.srow_stride +
-           (int64_t)(e >> 5) * 2;
+    const int idx = which ? slot * (o.head_dim >> 5) + (e >> 5) : q8ks_off(slot, e >> 5, o.head_dim);
+    return page * o.L.page_stride + (int64_t)h * o.L.head_stride + (int64_t)idx * 2;
 }
 
 // Byte offset of Q8_0 quant (row, element gi) of K (which = 0) or V (1); the
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(64) void write_rows_kernel(const RowOps o, const in
                 uint32_t b1 = (uint8_t)quantize_one(x[4 * j + 1], inv_d);
                 uint32_t b2 = (uint8_t)quantize_one(x[4 * j + 2], inv_d);
                 uint32_t b3 = (uint8_t)quantize_one(x[4 * j + 3], inv_d);
-                w[j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+                w[j] = (b0 | (b1 << 8) | (b2 << 16) | (b3 << 24)) ^ 0x80808080u;  // stored as x + 128
             }
             if (!which) {  // K: four 8-byte runs (d = gi0 + 8*kg .. +7)
 #pragma unroll
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(64) void write_rows_kernel(const RowOps o, const in
                 for (int j = 0; j < 32; j++) dst[q8_off(o, row, gi0 + j, 1)] = (uint8_t)(w[j >> 2] >> ((j & 3) * 8));
             }
             uint8_t *sb = const_cast<uint8_t *>(which ? o.L.vs : o.L.ks);
-            *reinterpret_cast<uint16_t *>(sb + scale_off(o, row, gi0)) = __half_as_ushort(__float2half_rn(dsc));
+            *reinterpret_cast<uint16_t *>(sb + scale_off(o, row, gi0, which)) = __half_as_ushort(__float2half_rn(dsc));
         }
     }
 }
@@ -142,11 +144,11 @@ __global__ __launch_bounds__(64) void export_rows_kernel(const RowOps o, const i
             const uint8_t *s = src + elem_off(o, row, gi0, 4);
             for (int j = 0; j < 128; j++) out[(int64_t)gi0 * 4 + j] = s[j];
         } else {
-            const uint8_t *sc = (which ? o.L.vs : o.L.ks) + scale_off(o, row, gi0);
+            const uint8_t *sc = (which ? o.L.vs : o.L.ks) + scale_off(o, row, gi0, which);
             uint8_t *ob = out + (int64_t)blk * 34;
             ob[0] = sc[0];
             ob[1] = sc[1];
-            for (int j = 0; j < 32; j++) ob[2 + j] = src[q8_off(o, row, gi0 + j, which)];
+            for (int j = 0; j < 32; j++) ob[2 + j] = src[q8_off(o, row, gi0 + j, which)] ^ 0x80;
         }
     }
 }
@@ -168,11 +170,11 @@ __global__ __launch_bounds__(64) void import_rows_kernel(const RowOps o, const i
             uint8_t *d = dst + elem_off(o, row, gi0, 4);
             for (int j = 0; j < 128; j++) d[j] = in[(int64_t)gi0 * 4 + j];
         } else {
-            uint8_t *sc = const_cast<uint8_t *>(which ? o.L.vs : o.L.ks) + scale_off(o, row, gi0);
+            uint8_t *sc = const_cast<uint8_t *>(which ? o.L.vs : o.L.ks) + scale_off(o, row, gi0, which);
             const uint8_t *ib = in + (int64_t)blk * 34;
             sc[0] = ib[0];
             sc[1] = ib[1];
-            for (int j = 0; j < 32; j++) dst[q8_off(o, row, gi0 + j, which)] = ib[2 + j];
+            for (int j = 0; j < 32; j++) dst[q8_off(o, row, gi0 + j, which)] = ib[2 + j] ^ 0x80;
         }
     }
 }
@@ -184,9 +186,15 @@ __global__ __launch_bounds__(256) void copy_bytes_kernel(const uint4 *src, uint4
         dst[i] = src[i];
 }
 
-__global__ __launch_bounds__(256) void zero_bytes_kernel(uint4 *dst, int64_t n16) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
-        dst[i] = make_uint4(0, 0, 0, 0);
+// Fill of whole pages: a 16-byte unit at byte offset o of its (page, head)
+// block of `head16` units gets `quant` below unit `quant16`, zero above (f32
+// pages: everything zero; Q8_0 pages: quants 0x80 = stored 0, scales 0).
+__global__ __launch_bounds__(256) void zero_bytes_kernel(uint4 *dst, int64_t n16, int64_t head16, int64_t quant16,
+                                                         uint32_t quant) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x) {
+        const uint32_t w = (i % head16) < quant16 ? quant : 0u;
+        dst[i] = make_uint4(w, w, w, w);
+    }
 }
 
 int check_launch(const char *what) {
@@ -237,8 +245,12 @@ int launch_copy_page(gla_ctx *ctx, gla_kv *kv, int64_t src, int64_t dst) {
 
 int launch_zero_pages(gla_ctx *ctx, gla_kv *kv, int64_t first, int64_t count) {
     const int64_t n16 = kv->page_bytes / 16 * count;
+    const int64_t head16 = kv->head_bytes / 16;
+    const bool q8 = kv->dtype == GLA_KV_Q8_0;
+    const int64_t quant16 = q8 ? (int64_t)GLA_PAGE_SIZE * kv->head_dim * 2 / 16 : 0;  // Kq and Vq
     uint4 *d = reinterpret_cast<uint4 *>(kv->base + first * kv->page_bytes);
-    hipLaunchKernelGGL(zero_bytes_kernel, dim3(grid_for(n16)), dim3(256), 0, ctx->stream, d, n16);
+    hipLaunchKernelGGL(zero_bytes_kernel, dim3(grid_for(n16)), dim3(256), 0, ctx->stream, d, n16, head16, quant16,
+                       0x80808080u);
     return check_launch("zero_bytes_kernel");
 }
 

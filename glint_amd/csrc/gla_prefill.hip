@@ -88,16 +88,17 @@ __device__ __forceinline__ void load_tile(const PrefillParams &p, int b, int kvh
                 for (int e = 0; e < 16; e++)
                     vw4[e >> 2] |= (uint32_t)p.kv.v[hb + q8v_off(slot, c16 * 16 + e, D)] << ((e & 3) * 8);
                 const uint4 vq = make_uint4(vw4[0], vw4[1], vw4[2], vw4[3]);
-                const int64_t sb = pid * p.kv.page_stride + head_off + (int64_t)slot * p.kv.srow_stride +
-                                   ((c16 * 16) >> 5) * 2;
-                const float ksc = __half2float(__ushort_as_half(*reinterpret_cast<const uint16_t *>(p.kv.ks + sb)));
-                const float vsc = __half2float(__ushort_as_half(*reinterpret_cast<const uint16_t *>(p.kv.vs + sb)));
+                const int blk = (c16 * 16) >> 5;
+                const uint16_t *ksp = reinterpret_cast<const uint16_t *>(p.kv.ks + hb) + q8ks_off(slot, blk, D);
+                const uint16_t *vsp = reinterpret_cast<const uint16_t *>(p.kv.vs + hb) + slot * (D / 32) + blk;
+                const float ksc = __half2float(__ushort_as_half(*ksp));
+                const float vsc = __half2float(__ushort_as_half(*vsp));
                 const uint32_t kw[4] = {kq.x, kq.y, kq.z, kq.w};
                 const uint32_t vw[4] = {vq.x, vq.y, vq.z, vq.w};
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    kf[e] = (float)(int8_t)((kw[e >> 2] >> ((e & 3) * 8)) & 0xff) * ksc;
-                    vf[e] = (float)(int8_t)((vw[e >> 2] >> ((e & 3) * 8)) & 0xff) * vsc;
+                for (int e = 0; e < 16; e++) {  // stored quants are x + 128
+                    kf[e] = (float)((int)((kw[e >> 2] >> ((e & 3) * 8)) & 0xff) - 128) * ksc;
+                    vf[e] = (float)((int)((vw[e >> 2] >> ((e & 3) * 8)) & 0xff) - 128) * vsc;
                 }
             } else {
                 const float4 *kp4 = reinterpret_cast<const float4 *>(p.kv.k + base) + c16 * 4;
