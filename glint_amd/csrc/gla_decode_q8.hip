@@ -458,34 +458,41 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
     const int npg = min(p.ch, r.fp + r.n_pages - pg0);
     const int nsteps = (npg + 1) >> 1;
 
-    // physical page of chunk page `lane` (clamped into the pool by map_page)
-    const int pid_l = (int)map_page(p.pm, b, pg0 + min(lane, npg - 1));
-    const uint8_t *head_base = p.base + (int64_t)kvh * p.head_stride;
-
-    // start streaming step 0; q and the V-scale scan overlap it
-    const uint32_t slot_lds = __builtin_amdgcn_readfirstlane(lds_addr(slot));
-    issue_step<D>(p, head_base, pid_l, 0, npg, lane, slot_lds);
-
-    // ---- Q as the B operand of S = K.Q ----
+    // q and the chunk's page ids are loaded together (the streaming loads
+    // below are a compiler barrier, so q must be requested before them)
     const int gq = (lc >> 1) & 3;  // head of this lane's column / row
     const int piece = lc & 1;
     const int ph = (lc >> 3) & 1;  // block parity of the column; page of the P' row
     const bool qvalid = gq < gcount;
-    float qx[NB][8];
-    float qmax = 0.0f;
+    float4 qraw[NB][2];
     {
         const float *qp = p.q + ((int64_t)b * p.n_heads + h_base + (qvalid ? gq : 0)) * D;
 #pragma unroll
         for (int blk = 0; blk < NB; blk++) {
-            const float4 a = *reinterpret_cast<const float4 *>(qp + blk * 32 + kg * 8);
-            const float4 e = *reinterpret_cast<const float4 *>(qp + blk * 32 + kg * 8 + 4);
-            const float t[8] = {a.x, a.y, a.z, a.w, e.x, e.y, e.z, e.w};
+            qraw[blk][0] = *reinterpret_cast<const float4 *>(qp + blk * 32 + kg * 8);
+            qraw[blk][1] = *reinterpret_cast<const float4 *>(qp + blk * 32 + kg * 8 + 4);
+        }
+    }
+    // physical page of chunk page `lane` (clamped into the pool by map_page)
+    const int pid_l = (int)map_page(p.pm, b, pg0 + min(lane, npg - 1));
+    const uint8_t *head_base = p.base + (int64_t)kvh * p.head_stride;
+
+    // start streaming the first step; the q split and the V-scale scan overlap it
+    const uint32_t slot_lds = __builtin_amdgcn_readfirstlane(lds_addr(slot));
+    issue_step<D>(p, head_base, pid_l, 0, npg, lane, slot_lds);
+
+    // ---- Q as the B operand of S = K.Q ----
+    float qx[NB][8];
+    float qmax = 0.0f;
 #pragma unroll
-            for (int s = 0; s < 8; s++) {
-                const float x = t[s] * p.q_mul;
-                qx[blk][s] = x;
-                qmax = fmaxf(qmax, fabsf(x));
-            }
+    for (int blk = 0; blk < NB; blk++) {
+        const float t[8] = {qraw[blk][0].x, qraw[blk][0].y, qraw[blk][0].z, qraw[blk][0].w,
+                            qraw[blk][1].x, qraw[blk][1].y, qraw[blk][1].z, qraw[blk][1].w};
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const float x = t[s] * p.q_mul;
+            qx[blk][s] = x;
+            qmax = fmaxf(qmax, fabsf(x));
         }
     }
     qmax = max_rows(qmax);
@@ -691,14 +698,32 @@ __global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p
     const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
     const int64_t pstride = (int64_t)kGT * (D + 2);
     const float *hp = p.part + unit * p.max_wg * pstride + g * (D + 2);
-    float M = -INFINITY;
-    for (int i = 0; i < n_wg; i++) M = fmaxf(M, hp[i * pstride + D]);
-    float L = 0.0f, A = 0.0f;
-    for (int i = 0; i < n_wg; i++) {
-        const float mi = hp[i * pstride + D];
-        const float f = (mi == -INFINITY) ? 0.0f : fast_exp2(mi - M);
-        L = fmaf(hp[i * pstride + D + 1], f, L);
-        A = fmaf(hp[i * pstride + d], f, A);
+    // one pass, eight partials at a time: all loads of a batch are in flight
+    // together, and (M, L, A) absorb the batch with one rescale
+    float M = -INFINITY, L = 0.0f, A = 0.0f;
+    for (int i0 = 0; i0 < n_wg; i0 += 8) {
+        float mi[8], li[8], ai[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = min(i0 + j, n_wg - 1);
+            mi[j] = (i0 + j < n_wg) ? hp[i * pstride + D] : -INFINITY;
+            li[j] = hp[i * pstride + D + 1];
+            ai[j] = hp[i * pstride + d];
+        }
+        float bm = M;
+#pragma unroll
+        for (int j = 0; j < 8; j++) bm = fmaxf(bm, mi[j]);
+        if (bm == -INFINITY) continue;
+        const float f0 = (M == -INFINITY) ? 0.0f : fast_exp2(M - bm);
+        L *= f0;
+        A *= f0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float f = (mi[j] == -INFINITY) ? 0.0f : fast_exp2(mi[j] - bm);
+            L = fmaf(li[j], f, L);
+            A = fmaf(ai[j], f, A);
+        }
+        M = bm;
     }
     p.out[((int64_t)b * p.n_heads + h_base + g) * D + d] = L > 0.0f ? A * (1.0f / L) : 0.0f;
 }
@@ -727,10 +752,11 @@ int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
     // pages a window can span (a start inside a page adds one)
     const int64_t max_pages = d.max_kv_len > 0 ? (d.max_kv_len + GLA_PAGE_SIZE - 1) / GLA_PAGE_SIZE + 1 : 1;
     const int64_t units = (int64_t)d.n_seqs * d.n_kv_heads * n_hg;
-    // Chunk size: about 16k wave-chunks over the longest sequence, preferring
-    // at most kMaxChunks chunks per unit; even and 2..64 pages (a wave holds
-    // one page id per lane).
-    int64_t ch = std::max<int64_t>(2, units * max_pages / 16384);
+    // Chunk size: about 8k wave-chunks over the longest sequence (a chunk's
+    // set-up costs a few memory round trips, so longer chunks pay off until
+    // the tail of the grid gets ragged), preferring at most kMaxChunks chunks
+    // per unit; even and 2..64 pages (a wave holds one page id per lane).
+    int64_t ch = std::max<int64_t>(2, units * max_pages / 8192);
     ch = std::max<int64_t>(ch, (max_pages + kMaxChunks - 1) / kMaxChunks);
     if (const char *env = getenv("GLA_Q8_CHUNK_PAGES")) {
         const int v = atoi(env);
