@@ -1,18 +1,28 @@
 """Benchmark of the gfx950 attention path on BASELINE.json's configurations.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg3|cfg2|cfg4|cfg5|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|cfg1|cfg2|cfg3|cfg4|cfg5]
+                    [--no-cpu] [--calibrate]
 
 Prints ONE JSON line. `value` is BASELINE's headline metric on its headline
 workload: achieved HBM GB/s of Llama-3-8B-shaped paged Q8_0 decode attention
-at batch 64 (config 3), inputs resident in HBM. The other configurations are
-reported under "secondary" (config 2: 32 layers of f32 decode; config 4:
-4x2048 causal prefill in TFLOP/s; config 5: Gemma-2 windowed + global decode).
+at batch 64 (config 3), with every input resident in HBM. The other
+configurations are reported under "secondary": config 1 (SmolLM decode
+latency), config 2 (32 layers of f32 decode), config 4 (4x2048 causal
+prefill, TFLOP/s) and config 5 (Gemma-2 windowed + global decode).
 
-Timing: W untimed steps, then K steps between two HIP events recorded on the
+A step is one gla_decode (or gla_prefill) call over the whole batch for one
+layer. W untimed steps, then K steps between two HIP events recorded on the
 library's stream (the stream the kernels run on), with a device
-synchronisation on both sides. A step is one attention call over the whole
-batch (one layer); consecutive steps alternate between layers whose K/V live
-in different memory, so the 256 MB Infinity Cache cannot serve repeats.
+synchronisation on both sides. Consecutive steps alternate between layers
+whose K/V live in different memory, so the 256 MB Infinity Cache cannot
+serve repeats.
+
+roofline: algorithmic bytes of one call (unique K/V bytes of the attended
+positions, page-table entries, q and out) divided by the call's average
+duration; the call is decode_q8_mfma_kernel + decode_q8_combine_kernel.
+`traffic` comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed
+in profiles/decode_q8_cfg3_pmc.md (calibrated against a page-copy kernel of
+known size, see --calibrate), or is null when that file is absent.
 
 cpu_baseline: the C restatement of Glint's CPU flash path (oracle/) on the
 same inputs, on the host cores, parallel over sequences as Glint's Rayon loop
@@ -24,6 +34,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -33,15 +44,16 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from glint_amd import _lib, synth  # noqa: E402
+from glint_amd import synth  # noqa: E402
 from glint_amd.attn import GpuBackend  # noqa: E402
 
 METRIC = "decode-attn HBM GB/s (% peak) + prefill TFLOP/s, Llama-3-8B GQA shape"
-HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 PAGE = 16
 SEED = 0x61F7
+PMC_SUMMARY = ROOT / "profiles" / "decode_q8_cfg3_pmc.md"
 
 
 def log(msg: str) -> None:
@@ -57,7 +69,6 @@ class HipEvents:
         self.h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
         self.h.hipEventSynchronize.argtypes = [C.c_void_p]
         self.h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
-        self.h.hipEventDestroy.argtypes = [C.c_void_p]
 
     def create(self):
         e = C.c_void_p()
@@ -88,8 +99,35 @@ def time_steps(be: GpuBackend, ev: HipEvents, step, steps: int, warmup: int) -> 
     return ev.elapsed_ms(e0, e1) / steps
 
 
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the box's cores, at most 16 (the share of one GPU)."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def q8_token_bytes(n_kv: int, d: int) -> int:
+    return 2 * n_kv * (d + (d // 32) * 2)  # K and V quants + f16 block scales
+
+
+def unique_rows(pb: synth.PagedBatch) -> tuple[int, int]:
+    """(unique physical rows read, logical rows read) by a decode over pb."""
+    rows = []
+    for b in range(len(pb.ctx)):
+        pos = np.arange(pb.kv_start[b], pb.kv_start[b] + pb.kv_len[b])
+        rows.append(pb.table[b, pos // PAGE].astype(np.int64) * PAGE + pos % PAGE)
+    allr = np.concatenate(rows) if rows else np.zeros(0, np.int64)
+    return int(len(np.unique(allr))), int(len(allr))
+
+
+def pages_read(pb: synth.PagedBatch) -> int:
+    n = 0
+    for b in range(len(pb.ctx)):
+        if pb.kv_len[b] > 0:
+            n += (int(pb.kv_start[b] + pb.kv_len[b] - 1) // PAGE) - int(pb.kv_start[b]) // PAGE + 1
+    return n
+
+
 def write_pool_chunked(pool, seed_k, seed_v, first_page, n_pages, kv_dim, k_mul=1.0, keep_q8=False):
-    """Generate N(0,1) rows page-chunk by page-chunk, write them (quantise-on-write) and
+    """Generate N(0,1) rows page-chunk by page-chunk and write them (quantise-on-write);
     optionally keep the host Q8_0 bytes (Glint's 34-byte blocks) for the CPU baseline."""
     chunk = max(1, (1 << 16) // PAGE)
     kq = vq = None
@@ -109,31 +147,10 @@ def write_pool_chunked(pool, seed_k, seed_v, first_page, n_pages, kv_dim, k_mul=
     return kq, vq
 
 
-def unique_rows(pb: synth.PagedBatch, table_offset: int = 0) -> tuple[int, int]:
-    """(unique physical rows read, logical rows read) by a decode over pb."""
-    rows = []
-    for b in range(len(pb.ctx)):
-        pos = np.arange(pb.kv_start[b], pb.kv_start[b] + pb.kv_len[b])
-        rows.append((pb.table[b, pos // PAGE].astype(np.int64) + table_offset) * PAGE + pos % PAGE)
-    allr = np.concatenate(rows) if rows else np.zeros(0, np.int64)
-    return int(len(np.unique(allr))), int(len(allr))
-
-
-def pages_read(pb: synth.PagedBatch) -> int:
-    n = 0
-    for b in range(len(pb.ctx)):
-        if pb.kv_len[b] > 0:
-            n += (int(pb.kv_start[b] + pb.kv_len[b] - 1) // PAGE) - int(pb.kv_start[b]) // PAGE + 1
-    return n
-
-
-def cpu_threads() -> int:
-    return max(1, min(16, os.cpu_count() or 1))
-
-
 # --------------------------------------------------------------------------- decode workloads
 class PagedDecode:
-    """Configs 3 and 5: batched decode over a paged Q8_0 pool, `n_layers` layers in one pool."""
+    """Configs 3 and 5: batched decode over a paged Q8_0 pool, one layer per entry of
+    `windows` (None: global attention), all layers in one pool."""
 
     def __init__(self, be, name, H, Hkv, d, B, ctx_lo, ctx_hi, prefix, softcap, windows, k_mul, seed):
         self.be, self.name, self.H, self.Hkv, self.d = be, name, H, Hkv, d
@@ -144,9 +161,9 @@ class PagedDecode:
         base = synth.paged_batch(seed + 1, self.ctx, prefix_tokens=prefix)
         self.n_layers = len(windows)
         self.layers = []
-        total_pages = base.n_pages * self.n_layers
-        self.pool = be.create_page_pool(total_pages, Hkv, d, "q8")
+        self.pool = be.create_page_pool(base.n_pages * self.n_layers, Hkv, d, "q8")
         self.host_q8 = None
+        tok = q8_token_bytes(Hkv, d)
         for li, w in enumerate(windows):
             pb = synth.windowed(base, w)
             table = pb.table + li * base.n_pages
@@ -156,15 +173,13 @@ class PagedDecode:
                 self.host_q8 = (kq, vq, pb)
             q = synth.normal(synth.tensor_seed(seed, 3, li, 3), (B, H, d))
             uniq, logical = unique_rows(pb)
-            bytes_kv = uniq * 2 * Hkv * (d + (d // 32) * 2)
             self.layers.append(dict(
-                pb=pb,
-                q=be.buffer(q), q_host=q, out=be.empty(q.nbytes),
+                pb=pb, q=be.buffer(q), q_host=q, out=be.empty(q.nbytes),
                 start=be.buffer(pb.kv_start), len=be.buffer(pb.kv_len), table=be.buffer(table),
                 stride=table.shape[1], max_len=int(pb.kv_len.max()),
-                bytes=bytes_kv + pages_read(pb) * 4 + 2 * q.nbytes,
-                bytes_logical=logical * 2 * Hkv * (d + (d // 32) * 2) + pages_read(pb) * 4 + 2 * q.nbytes,
-                flops=4 * H * d * int(pb.kv_len.sum()),
+                bytes=uniq * tok + pages_read(pb) * 4 + 2 * q.nbytes,
+                bytes_logical=logical * tok + pages_read(pb) * 4 + 2 * q.nbytes,
+                attended=int(pb.kv_len.sum()),
             ))
         be.sync()
 
@@ -176,7 +191,7 @@ class PagedDecode:
     def bytes_per_step(self):
         return float(np.mean([L["bytes"] for L in self.layers]))
 
-    def cpu_baseline(self, min_seconds=10.0):
+    def cpu_baseline(self, min_seconds=10.0, max_reps=50):
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as orc
         kq, vq, pb = self.host_q8
@@ -192,26 +207,26 @@ class PagedDecode:
                              self.softcap, n_threads=nt)
             reps += 1
             el = time.perf_counter() - t0
-            if el >= min_seconds or reps >= 50:
+            if el >= min_seconds or reps >= max_reps:
                 break
         return dict(value=round(L0["bytes"] * reps / el / 1e9, 3), unit="GB/s", cores=nt, kind="port",
                     sample=f"{reps} x layer 0 of {self.name} (all {len(self.ctx)} sequences, same inputs), "
-                           f"{el:.1f} s")
+                           f"{el:.1f} s; oracle/glint_oracle.c decode_batch, one thread per sequence")
 
 
 class ContigDecode:
-    """Config 2: single-sequence f32 decode, 32 layers back to back (1 GiB of K/V)."""
+    """Configs 1 and 2: single-sequence f32 decode over contiguous caches, `n_layers`
+    layers back to back with independent seeds (config 2: 32 layers = 1 GiB of K/V)."""
 
-    def __init__(self, be, n_layers=32, ctx=4096, H=32, Hkv=8, d=128, seed=0x2222):
-        self.be, self.H, self.Hkv, self.d, self.ctx = be, H, Hkv, d, ctx
+    def __init__(self, be, n_layers, ctx, H, Hkv, d, seed, name):
+        self.be, self.H, self.Hkv, self.d, self.ctx, self.name = be, H, Hkv, d, ctx, name
         self.kv_dim = Hkv * d
         self.n_layers = n_layers
         self.scale = float(1.0 / np.sqrt(d))
         self.cache = be.create_kv_cache(n_layers, ctx, Hkv, d, "f32", 1)
-        ppl = (ctx + PAGE - 1) // PAGE
         self.host = None
         for layer in range(n_layers):
-            rows = (layer * ppl * PAGE + np.arange(ctx)).astype(np.int64)
+            rows = np.array([self.cache.row_id(0, layer, 0)], np.int64) + np.arange(ctx)
             k = synth.normal_rows(synth.tensor_seed(seed, 2, layer, 1), ctx, self.kv_dim)
             v = synth.normal_rows(synth.tensor_seed(seed, 2, layer, 2), ctx, self.kv_dim)
             for i in range(0, ctx, 1 << 14):
@@ -233,7 +248,7 @@ class ContigDecode:
     def bytes_per_step(self):
         return float(2 * self.ctx * self.kv_dim * 4 + 2 * self.H * self.d * 4)
 
-    def cpu_baseline(self, min_seconds=5.0):
+    def cpu_baseline(self, min_seconds=3.0, max_reps=2000):
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as orc
         k, v = self.host
@@ -244,28 +259,27 @@ class ContigDecode:
             orc.attn_heads_cpu(q, st, 0, 0, self.ctx, self.H, self.H // self.Hkv, self.d, self.scale)
             reps += 1
             el = time.perf_counter() - t0
-            if el >= min_seconds or reps >= 200:
+            if el >= min_seconds or reps >= max_reps:
                 break
         return dict(value=round(self.bytes_per_step() * reps / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
-                    sample=f"{reps} x layer 0 (attn_heads_cpu, serial over heads as Glint), {el:.1f} s")
+                    sample=f"{reps} x layer 0 of {self.name} (attn_heads_cpu, serial over heads as Glint), "
+                           f"{el:.1f} s", us_per_layer=round(el / reps * 1e6, 2))
 
 
 class Prefill:
-    """Config 4: causal prefill of 4 prompts x 2048, f32 KV cache."""
+    """Config 4: causal prefill of 4 prompts x 2048 over an f32 KV cache (2 layers alternating)."""
 
-    def __init__(self, be, precision="f32", B=4, S=2048, H=32, Hkv=8, d=128, seed=0x4444):
+    def __init__(self, be, B=4, S=2048, H=32, Hkv=8, d=128, seed=0x4444):
         self.be, self.B, self.S, self.H, self.Hkv, self.d = be, B, S, H, Hkv, d
-        self.precision = precision
         self.kv_dim = Hkv * d
         self.scale = float(1.0 / np.sqrt(d))
         self.n_layers = 2
         self.cache = be.create_kv_cache(self.n_layers, S, Hkv, d, "f32", B)
-        ppl = (S + PAGE - 1) // PAGE
         self.host = None
         self.q = []
         for layer in range(self.n_layers):
             for b in range(B):
-                rows = (((b * self.n_layers + layer) * ppl) * PAGE + np.arange(S)).astype(np.int64)
+                rows = np.array([self.cache.row_id(b, layer, 0)], np.int64) + np.arange(S)
                 k = synth.normal_rows(synth.tensor_seed(seed, 4, layer * 8 + b, 1), S, self.kv_dim)
                 v = synth.normal_rows(synth.tensor_seed(seed, 4, layer * 8 + b, 2), S, self.kv_dim)
                 self.cache.write_rows(rows, k, v)
@@ -278,6 +292,7 @@ class Prefill:
         self.out = be.empty(B * S * H * d * 4)
         self.q_start = be.buffer(np.arange(B + 1, dtype=np.int32) * S)
         self.pos = be.buffer(np.zeros(B, np.int32))
+        self.precision = "f32"
         be.sync()
 
     def step(self, i):
@@ -288,125 +303,163 @@ class Prefill:
     def flops_per_step(self):
         return float(4 * self.B * self.H * self.d * self.S * (self.S + 1) // 2)
 
-    def cpu_baseline(self, rows=256):
+    def cpu_baseline(self, min_seconds=5.0, max_reps=20):
+        """Prompt 0 of layer 0 through the oracle's prefill, one task per query position on the
+        host cores as forward.rs:927-931."""
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as orc
         k, v = self.host
         st = orc.kv_cache(k[None], v[None])
-        # a sample of query rows spread over prompt 0 (cost grows with the position)
-        lp = np.linspace(0, self.S - 1, rows).astype(int)
+        q = self.q0_host[:self.S].reshape(self.S, -1)
         nt = cpu_threads()
-        t0 = time.perf_counter()
-        flops = 0
-        for start in range(0, rows, nt):
-            sel = lp[start:start + nt]
-            # one task per query position, as forward.rs:927-931
-            for p in sel:
-                pass
-            q = self.q0_host[sel].reshape(len(sel), -1)
-            for j, p in enumerate(sel):
-                orc.attn_heads_cpu(q[j], st, 0, 0, int(p) + 1, self.H, self.H // self.Hkv, self.d, self.scale)
-                flops += 4 * self.H * self.d * (int(p) + 1)
-        el = time.perf_counter() - t0
-        return dict(value=round(flops / el / 1e12, 6), unit="TFLOP/s", cores=1, kind="port",
-                    sample=f"{rows} query rows of prompt 0 spread over positions 0..{self.S - 1}, {el:.1f} s")
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            orc.prefill(q, st, 0, 0, self.H, self.Hkv, self.d, self.scale, n_threads=nt)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= min_seconds or reps >= max_reps:
+                break
+        flops = 4 * self.H * self.d * self.S * (self.S + 1) // 2 * reps
+        return dict(value=round(flops / el / 1e12, 6), unit="TFLOP/s", cores=nt, kind="port",
+                    sample=f"{reps} x prompt 0 of layer 0 ({self.S} positions, causal), oracle prefill, one task "
+                           f"per query position, {el:.1f} s")
+
+
+def calibrate(be: GpuBackend, n_copies: int = 2048) -> dict:
+    """Known-size copies for the FETCH_SIZE / WRITE_SIZE scale: gla_pool_copy_page on a
+    Q8_0 pool of the cfg3 shape copies one page (34,816 bytes read and written) per dispatch."""
+    pool = be.create_page_pool(2 * n_copies, 8, 128, "q8")
+    for i in range(n_copies):
+        pool.copy_page(i, n_copies + i)
+    be.sync()
+    nbytes = 8 * 34 * 128
+    pool.destroy()
+    return {"kernel": "copy_bytes_kernel", "dispatches": n_copies, "bytes_read_per_dispatch": nbytes,
+            "bytes_written_per_dispatch": nbytes}
+
+
+def traffic_from_profile() -> tuple[int | None, str | None]:
+    """HBM bytes per decode call from the committed rocprofv3 counter summary, if any."""
+    if not PMC_SUMMARY.exists():
+        return None, None
+    m = re.search(r"^traffic_bytes_per_call:\s*(\d+)", PMC_SUMMARY.read_text(), re.M)
+    return (int(m.group(1)), str(PMC_SUMMARY.relative_to(ROOT))) if m else (None, None)
 
 
 # --------------------------------------------------------------------------- main
-def run_decode(be, ev, wl, steps, warmup, peak=HBM_PEAK_GBS):
-    ms = time_steps(be, ev, wl.step, steps, warmup)
-    gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
-    return ms, gbs, gbs / peak
-
-
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="all", choices=["cfg2", "cfg3", "cfg4", "cfg5", "all"])
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--workload", default="all", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "all"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--calibrate", action="store_true", help="also run known-size page copies (for PMC runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build measures one GPU: the attention path has no multi-GPU leg; "
-                                   "run with --gpus 1"}))
+        print(json.dumps({"error": "this build measures one GPU: the attention path has no multi-GPU leg "
+                                   "(sharding is described in DESIGN.md); run with --gpus 1"}))
         return 2
 
     be = GpuBackend(0)
     ev = HipEvents()
+    want = {args.workload} if args.workload != "all" else {"cfg1", "cfg2", "cfg3", "cfg4", "cfg5"}
     result = {
         "metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (seeded Xorshift64 + Box-Muller, N(0,1) Q/K/V)",
+        "data": "synthetic (seeded Xorshift64 + Box-Muller, N(0,1) Q/K/V; K x3 for config 5)",
     }
     secondary = {}
-    want = {args.workload} if args.workload != "all" else {"cfg2", "cfg3", "cfg4", "cfg5"}
 
     if "cfg3" in want:
-        log("cfg3: building paged Q8_0 pool (2 layers, B=64)")
+        log("cfg3: paged Q8_0 pool, 2 layers, B=64")
         wl = PagedDecode(be, "cfg3", 32, 8, 128, 64, 128, 8192, 256, None, [None, None], 1.0, SEED + 3)
-        ms, gbs, frac = run_decode(be, ev, wl.step, args.steps, args.warmup) if False else run_decode(be, ev, wl, args.steps, args.warmup)
-        L0 = wl.layers[0]
+        ms = time_steps(be, ev, wl.step, args.steps, args.warmup)
+        gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
+        traffic, src = traffic_from_profile()
         result.update(value=round(gbs, 2), ms_per_step=round(ms, 5))
         result["config"] = {
             "workload": "cfg3: Llama-3-8B decode attention, paged Q8_0 KV, B=64, ctx U[128,8192], 16-token pages, "
-                        "256-token shared prefix, one layer per step (2 layers alternating)",
+                        "256-token shared prefix; one step = one layer's gla_decode for the batch (2 layers "
+                        "alternating)",
             "n_heads": 32, "n_kv_heads": 8, "head_dim": 128, "batch": 64, "kv_format": "q8_0 paged",
             "sum_ctx": int(wl.ctx.sum()), "bytes_per_step_unique": int(wl.bytes_per_step()),
             "bytes_per_step_logical": int(np.mean([L["bytes_logical"] for L in wl.layers])),
         }
-        result["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                              "frac": round(frac, 4), "traffic": None,
-                              "kernel": "decode_split_kernel<128,4,q8> + decode_combine_kernel (one step)"}
+        result["roofline"] = {
+            "bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": "decode_q8_mfma_kernel<128> + decode_q8_combine_kernel<128> (one gla_decode call)",
+            "algorithmic_bytes_per_call": int(wl.bytes_per_step()),
+            "us_per_call": round(ms * 1e3, 2),
+        }
+        if src:
+            result["roofline"]["traffic_source"] = src
+        log(f"cfg3: {ms * 1e3:.1f} us/call, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of peak)")
         if not args.no_cpu:
             log("cfg3: CPU baseline (oracle, same inputs)")
             result["cpu_baseline"] = wl.cpu_baseline()
-        log(f"cfg3: {ms * 1e3:.1f} us/step, {gbs:.1f} GB/s ({100 * frac:.1f}% of peak)")
+        del wl
+    if "cfg5" in want:
+        log("cfg5: Gemma-2 paged Q8_0 pool (windowed + global layer)")
+        wl = PagedDecode(be, "cfg5", 16, 8, 256, 32, 2048, 8192, 0, 50.0, [4096, None], 3.0, SEED + 5)
+        ms = time_steps(be, ev, wl.step, args.steps, args.warmup)
+        gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
+        secondary["cfg5"] = {
+            "workload": "Gemma-2-9B decode, paged Q8_0, B=32, ctx U[2048,8192], soft-cap 50, window 4096 and "
+                        "global layers alternating (one step = one layer)",
+            "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        if not args.no_cpu:
+            secondary["cfg5"]["cpu_baseline"] = wl.cpu_baseline(min_seconds=5.0, max_reps=10)
+        log(f"cfg5: {ms * 1e3:.1f} us/layer, {gbs:.1f} GB/s")
         del wl
     if "cfg2" in want:
-        log("cfg2: building 32-layer f32 cache")
-        wl = ContigDecode(be)
-        ms, gbs, frac = run_decode(be, ev, wl, max(args.steps, 64), args.warmup)
-        secondary["cfg2"] = {"workload": "Llama-3-8B single-sequence decode, f32 contiguous ctx 4096, 32 layers back to back",
-                             "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
-                             "frac_of_hbm_peak": round(frac, 4)}
+        log("cfg2: 32-layer f32 cache")
+        wl = ContigDecode(be, 32, 4096, 32, 8, 128, 0x2222, "cfg2")
+        ms = time_steps(be, ev, wl.step, max(args.steps, 64), args.warmup)
+        gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
+        secondary["cfg2"] = {
+            "workload": "Llama-3-8B single-sequence decode, f32 contiguous ctx 4096, 32 layers back to back",
+            "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         if not args.no_cpu:
             secondary["cfg2"]["cpu_baseline"] = wl.cpu_baseline()
         log(f"cfg2: {ms * 1e3:.1f} us/layer, {gbs:.1f} GB/s")
         del wl
+    if "cfg1" in want:
+        log("cfg1: SmolLM-135M decode, f32 ctx 512")
+        wl = ContigDecode(be, 8, 512, 9, 3, 64, 0x1111, "cfg1")
+        ms = time_steps(be, ev, wl.step, max(args.steps, 64), args.warmup)
+        secondary["cfg1"] = {
+            "workload": "SmolLM-135M decode, H9/KV3 d64, B=1, f32 contiguous ctx 512 (latency)",
+            "value": round(ms * 1e3, 2), "unit": "us/call",
+            "GB_per_s": round(wl.bytes_per_step() / (ms * 1e-3) / 1e9, 2)}
+        if not args.no_cpu:
+            secondary["cfg1"]["cpu_baseline"] = wl.cpu_baseline(min_seconds=2.0, max_reps=20000)
+        log(f"cfg1: {ms * 1e3:.2f} us/call")
+        del wl
     if "cfg4" in want:
-        log("cfg4: building 4x2048 prefill")
-        wl = Prefill(be, "f32")
-        ms = time_steps(be, ev, wl.step, max(3, args.steps // 10), min(args.warmup, 2))
+        log("cfg4: 4x2048 causal prefill, f32 KV cache")
+        wl = Prefill(be)
+        ms = time_steps(be, ev, wl.step, max(3, args.steps // 5), min(args.warmup, 2))
         tf = wl.flops_per_step() / (ms * 1e-3) / 1e12
-        secondary["cfg4_f32"] = {"workload": "Llama-3-8B causal prefill 4x2048, f32 KV cache, fp32 MFMA",
-                                 "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
-                                 "frac_of_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+        secondary["cfg4_f32"] = {
+            "workload": "Llama-3-8B causal prefill 4x2048, f32 KV cache, fp32-input MFMA",
+            "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+            "frac_of_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
         if not args.no_cpu:
             secondary["cfg4_f32"]["cpu_baseline"] = wl.cpu_baseline()
-        log(f"cfg4: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
-        if args.workload == "cfg4":
-            result.update(value=round(tf, 3), unit="TFLOP/s", ms_per_step=round(ms, 5))
-            result["config"] = {"workload": secondary["cfg4_f32"]["workload"]}
-            result["roofline"] = {"bound": "mfma", "achieved": round(tf, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
-                                  "unit": "TFLOP/s", "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None}
+        log(f"cfg4 f32: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
         del wl
-    if "cfg5" in want:
-        log("cfg5: building Gemma-2 paged Q8_0 pool (windowed + global layer)")
-        wl = PagedDecode(be, "cfg5", 16, 8, 256, 32, 2048, 8192, 0, 50.0, [4096, None], 3.0, SEED + 5)
-        ms, gbs, frac = run_decode(be, ev, wl, args.steps, args.warmup)
-        secondary["cfg5"] = {"workload": "Gemma-2-9B decode, paged Q8_0, B=32, ctx U[2048,8192], soft-cap 50, "
-                                         "window 4096 and global layers alternating",
-                             "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
-                             "frac_of_hbm_peak": round(frac, 4)}
-        log(f"cfg5: {ms * 1e3:.1f} us/layer, {gbs:.1f} GB/s")
-        del wl
-    if result["value"] is None and args.workload in ("cfg2", "cfg5"):
-        s = secondary[args.workload]
-        result.update(value=s["value"], ms_per_step=s["us_per_layer"] / 1e3)
+    if args.calibrate:
+        log("calibration copies")
+        result["calibration"] = calibrate(be)
+
+    if result["value"] is None:  # a single secondary workload was asked for: report it as the line
+        name, s = next(iter(secondary.items()))
+        result.update(value=s["value"], unit=s["unit"], ms_per_step=s.get("ms_per_step", s.get("us_per_layer", 0) / 1e3))
         result["config"] = {"workload": s["workload"]}
-        result["roofline"] = {"bound": "hbm", "achieved": s["value"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                              "frac": s["frac_of_hbm_peak"], "traffic": None}
     if secondary:
         result["secondary"] = secondary
     print(json.dumps(result), flush=True)

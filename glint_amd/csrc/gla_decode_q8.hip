@@ -195,7 +195,7 @@ struct Raw {
 //
 // Each wave streams its chunk through one LDS slot of two pages:
 // K_a | K_b | V_a | V_b (16*D bytes each, byte copies of the (page, head)
-// quant blocks) and the scales Ks_a | Ks_b | Vs_a | Vs_b (D bytes each). At
+// quant blocks: lane l's piece c at c*1024 + l*16) and the scales Ks_a | Ks_b | Vs_a | Vs_b (D bytes each). At
 // the top of a step the wave copies the slot into registers and refills it
 // with the next step, which is then in flight while this step computes.
 // The loads are issued from inline assembly with explicit vmcnt waits: the
@@ -251,13 +251,13 @@ __device__ __forceinline__ void issue_step(const Q8Params &p, const uint8_t *hea
     const int idb = __builtin_amdgcn_readlane(pid_l, pb);
     const uint8_t *ba = head_base + (int64_t)ida * p.page_stride;
     const uint8_t *bb = head_base + (int64_t)idb * p.page_stride;
-    // lane l's operand bytes [l*D/4, (l+1)*D/4) land as NQ pieces 1 KB apart
+    // byte copies of the quant blocks, one contiguous kilobyte per load
 #pragma unroll
     for (int c = 0; c < NQ; c++) {
-        dma16(ba + lane * (D / 4) + c * 16, slot + 0 * 16 * D + c * 1024);
-        dma16(bb + lane * (D / 4) + c * 16, slot + 1 * 16 * D + c * 1024);
-        dma16(ba + 16 * D + lane * (D / 4) + c * 16, slot + 2 * 16 * D + c * 1024);
-        dma16(bb + 16 * D + lane * (D / 4) + c * 16, slot + 3 * 16 * D + c * 1024);
+        dma16(ba + c * 1024 + lane * 16, slot + 0 * 16 * D + c * 1024);
+        dma16(bb + c * 1024 + lane * 16, slot + 1 * 16 * D + c * 1024);
+        dma16(ba + 16 * D + c * 1024 + lane * 16, slot + 2 * 16 * D + c * 1024);
+        dma16(bb + 16 * D + c * 1024 + lane * 16, slot + 3 * 16 * D + c * 1024);
     }
     // scales, byte-identical: [Ks_a | Ks_b | Vs_a | Vs_b], 256 bytes per load
 #pragma unroll

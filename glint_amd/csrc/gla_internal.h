@@ -18,12 +18,15 @@
 //
 // Q8_0 quants are stored as x + 128 (sign bit flipped; a zeroed page holds
 // 0x80 bytes) in the order the MFMA decode kernel consumes them (q8k_off /
-// q8v_off below): lane l of a wave reads bytes [l*D/4, (l+1)*D/4) of a
-// (page, head) K or V block and gets exactly its MFMA operand bytes.
+// q8v_off below). A (page, head) K or V block is D/64 pieces of 1 KB; lane l
+// of a wave finds its 16 operand bytes of piece c at c*1024 + l*16, so one
+// 16-byte-per-lane load moves a contiguous kilobyte.
 //   K[slot t][d]: lane (kg = (d>>3)&3)*16 + t holds, for each 32-block
-//                 blk = d>>5, the 8 bytes d = blk*32 + kg*8 + 0..7.
+//                 blk = d>>5, the 8 bytes d = blk*32 + kg*8 + 0..7
+//                 (piece blk>>1, bytes (blk&1)*8 ..).
 //   V[slot s][d]: lane (s>>2)*16 + (d&15) holds, for each 16-wide d tile
-//                 dt = d>>4, the 4 bytes of slots (s & ~3) + 0..3.
+//                 dt = d>>4, the 4 bytes of slots (s & ~3) + 0..3
+//                 (piece dt>>2, bytes (dt&3)*4 ..).
 // K scales are grouped by block parity, Ks[blk & 1][slot][blk >> 1]
 // (q8ks_off), V scales are row-major, Vs[slot][blk], all f16.
 #pragma once
@@ -83,12 +86,12 @@ struct PageMap {
 // Byte offset of quant K[slot][d] / V[slot][d] inside a (page, head) Q8_0
 // quant block of head_dim D (16*D bytes).
 __host__ __device__ __forceinline__ int q8k_off(int slot, int d, int D) {
-    const int nb = D >> 5;
-    return ((((d >> 3) & 3) * 16 + slot) * nb + (d >> 5)) * 8 + (d & 7);
+    (void)D;
+    return (d >> 6) * 1024 + (((d >> 3) & 3) * 16 + slot) * 16 + ((d >> 5) & 1) * 8 + (d & 7);
 }
 __host__ __device__ __forceinline__ int q8v_off(int slot, int d, int D) {
-    const int nd = D >> 4;
-    return (((slot >> 2) * 16 + (d & 15)) * nd + (d >> 4)) * 4 + (slot & 3);
+    (void)D;
+    return (d >> 6) * 1024 + ((slot >> 2) * 16 + (d & 15)) * 16 + ((d >> 4) & 3) * 4 + (slot & 3);
 }
 // f16 index of the K scale of (slot, block) inside a (page, head) Ks array.
 __host__ __device__ __forceinline__ int q8ks_off(int slot, int blk, int D) {
