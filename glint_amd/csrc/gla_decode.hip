@@ -13,8 +13,8 @@
 //   tokens. A lane group keeps its own online-softmax state (m, l, acc) in
 //   the log2 domain; the groups are merged with shuffles once per split, the
 //   4 waves through LDS, and splits by decode_combine_kernel.
-//   Q8_0 blocks are dequantised in registers: the lane's chunk lies inside
-//   one 32-element block, so the block scale multiplies the partial dot once.
+// This file serves f32 storage; Q8_0 storage has its own MFMA kernel
+// (gla_decode_q8.hip).
 #include <float.h>
 #include <math.h>
 #include <stdlib.h>
@@ -30,6 +30,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kStepsPerIter = 2;  // half-page token steps a lane group loads per iteration
 
 struct DecodeParams {
     KvLayout kv;
@@ -100,57 +101,16 @@ __device__ __forceinline__ SeqRange seq_range(const DecodeParams &p, int b) {
     return r;
 }
 
-template <int CB>
-struct Chunk;
-template <>
-struct Chunk<16> {
-    using T = uint4;
-};
-template <>
-struct Chunk<8> {
-    using T = uint2;
-};
-
-template <int CB>
-__device__ __forceinline__ typename Chunk<CB>::T zero_chunk();
-template <>
-__device__ __forceinline__ uint4 zero_chunk<16>() {
-    return make_uint4(0, 0, 0, 0);
-}
-template <>
-__device__ __forceinline__ uint2 zero_chunk<8>() {
-    return make_uint2(0, 0);
+__device__ __forceinline__ float word_f(const uint4 &c, int w) {
+    return __uint_as_float(w == 0 ? c.x : (w == 1 ? c.y : (w == 2 ? c.z : c.w)));
 }
 
-__device__ __forceinline__ uint32_t chunk_word(const uint4 &c, int w) {
-    return w == 0 ? c.x : (w == 1 ? c.y : (w == 2 ? c.z : c.w));
-}
-__device__ __forceinline__ uint32_t chunk_word(const uint2 &c, int w) { return w == 0 ? c.x : c.y; }
-
-// Element e of a chunk as float: f32 chunks hold 4 floats, Q8 chunks 8 or 16
-// signed bytes.
-template <bool Q8, typename T>
-__device__ __forceinline__ float chunk_elem(const T &c, int e) {
-    if constexpr (Q8) {
-        uint32_t w = chunk_word(c, e >> 2);
-        return (float)(int8_t)((w >> ((e & 3) * 8)) & 0xff);
-    } else {
-        return __uint_as_float(chunk_word(c, e));
-    }
-}
-
-__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
-    return __half2float(__ushort_as_half(h));
-}
-
-template <int D, int GT, bool Q8, int NSTEP>
+template <int D, int GT, int NSTEP>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodeParams p) {
-    constexpr int EPL = D / 8;                    // elements per lane
-    constexpr int CB = (Q8 && D == 64) ? 8 : 16;  // bytes per chunk load
-    constexpr int EPC = Q8 ? CB : CB / 4;         // elements per chunk
-    constexpr int NCH = EPL / EPC;                // chunks per lane
-    constexpr int PPW = NSTEP / 2;                // pages per wave per iteration
-    using CT = typename Chunk<CB>::T;
+    constexpr int EPL = D / 8;       // elements per lane
+    constexpr int EPC = 4;           // floats per 16-byte chunk
+    constexpr int NCH = EPL / EPC;   // chunks per lane
+    constexpr int PPW = NSTEP / 2;   // pages per wave per iteration
 
     __shared__ float lds_acc[kWaves][GT][D];
     __shared__ float lds_m[kWaves][GT];
@@ -207,8 +167,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
     const int64_t head_off = (int64_t)kvh * p.kv.head_stride;
 
     for (int pb = pg0 + wave * PPW; pb < pg1; pb += kWaves * PPW) {
-        CT kr[NSTEP][NCH], vr[NSTEP][NCH];
-        float ks[NSTEP][NCH], vs[NSTEP][NCH];
+        uint4 kr[NSTEP][NCH], vr[NSTEP][NCH];
         bool valid[NSTEP];
         int64_t pid[PPW];
 #pragma unroll
@@ -224,17 +183,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
             const uint8_t *vp = p.kv.v + base;
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
-                kr[s][i] = *reinterpret_cast<const CT *>(kp + (i * 8 + sub) * CB);
-                vr[s][i] = *reinterpret_cast<const CT *>(vp + (i * 8 + sub) * CB);
-            }
-            if constexpr (Q8) {
-                const int64_t sbase = pid[s / 2] * p.kv.page_stride + head_off + (int64_t)slot * p.kv.srow_stride;
-#pragma unroll
-                for (int i = 0; i < NCH; i++) {
-                    const int blk = ((i * 8 + sub) * EPC) >> 5;
-                    ks[s][i] = half_bits_to_float(*reinterpret_cast<const uint16_t *>(p.kv.ks + sbase + blk * 2));
-                    vs[s][i] = half_bits_to_float(*reinterpret_cast<const uint16_t *>(p.kv.vs + sbase + blk * 2));
-                }
+                kr[s][i] = *reinterpret_cast<const uint4 *>(kp + (i * 8 + sub) * 16);
+                vr[s][i] = *reinterpret_cast<const uint4 *>(vp + (i * 8 + sub) * 16);
             }
         }
 
@@ -247,21 +197,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
             for (int g = 0; g < GT; g++) dot[g] = 0.0f;
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
-                float part[GT];
-#pragma unroll
-                for (int g = 0; g < GT; g++) part[g] = 0.0f;
 #pragma unroll
                 for (int e = 0; e < EPC; e++) {
-                    const float kf = chunk_elem<Q8>(kr[s][i], e);
+                    const float kf = word_f(kr[s][i], e);
 #pragma unroll
-                    for (int g = 0; g < GT; g++) part[g] = fmaf(qv[g][i * EPC + e], kf, part[g]);
-                }
-#pragma unroll
-                for (int g = 0; g < GT; g++) {
-                    if constexpr (Q8)
-                        dot[g] = fmaf(part[g], ks[s][i], dot[g]);
-                    else
-                        dot[g] += part[g];
+                    for (int g = 0; g < GT; g++) dot[g] = fmaf(qv[g][i * EPC + e], kf, dot[g]);
                 }
             }
 #pragma unroll
@@ -293,10 +233,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
         for (int s = 0; s < NSTEP; s++) {
             if (!valid[s]) {
 #pragma unroll
-                for (int i = 0; i < NCH; i++) {
-                    vr[s][i] = zero_chunk<CB>();
-                    if constexpr (Q8) vs[s][i] = 0.0f;
-                }
+                for (int i = 0; i < NCH; i++) vr[s][i] = make_uint4(0, 0, 0, 0);
             }
             float pw[GT];
 #pragma unroll
@@ -306,14 +243,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
             }
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
-                float pv[GT];
-#pragma unroll
-                for (int g = 0; g < GT; g++) pv[g] = Q8 ? pw[g] * vs[s][i] : pw[g];
 #pragma unroll
                 for (int e = 0; e < EPC; e++) {
-                    const float vf = chunk_elem<Q8>(vr[s][i], e);
+                    const float vf = word_f(vr[s][i], e);
 #pragma unroll
-                    for (int g = 0; g < GT; g++) acc[g][i * EPC + e] = fmaf(pv[g], vf, acc[g][i * EPC + e]);
+                    for (int g = 0; g < GT; g++) acc[g][i * EPC + e] = fmaf(pw[g], vf, acc[g][i * EPC + e]);
                 }
             }
         }
@@ -417,10 +351,9 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(const DecodePa
     }
 }
 
-template <int D, int GT, bool Q8>
+template <int D, int GT>
 int launch_typed(gla_ctx *ctx, const DecodeParams &prm, dim3 grid, bool combine) {
-    constexpr int NSTEP = Q8 ? 4 : 2;
-    hipLaunchKernelGGL((decode_split_kernel<D, GT, Q8, NSTEP>), grid, dim3(kThreads), 0, ctx->stream, prm);
+    hipLaunchKernelGGL((decode_split_kernel<D, GT, kStepsPerIter>), grid, dim3(kThreads), 0, ctx->stream, prm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "decode_split_kernel launch: %s", hipGetErrorString(e));
     if (combine) {
@@ -431,12 +364,6 @@ int launch_typed(gla_ctx *ctx, const DecodeParams &prm, dim3 grid, bool combine)
             return set_error(GLA_ERR_KERNEL, "decode_combine_kernel launch: %s", hipGetErrorString(e));
     }
     return GLA_OK;
-}
-
-template <int D, int GT>
-int launch_dtype(gla_ctx *ctx, bool q8, const DecodeParams &prm, dim3 grid, bool combine) {
-    (void)q8;  // Q8_0 storage goes to the MFMA kernel (gla_decode_q8.hip)
-    return launch_typed<D, GT, false>(ctx, prm, grid, combine);
 }
 
 // Head-group width: the registers of a lane hold GT*(D/8) q values and as
@@ -450,20 +377,20 @@ int pick_gt(int d, int group) {
 }
 
 template <int D>
-int launch_d(gla_ctx *ctx, int gt, bool q8, const DecodeParams &prm, dim3 grid, bool combine) {
+int launch_d(gla_ctx *ctx, int gt, const DecodeParams &prm, dim3 grid, bool combine) {
     switch (gt) {
     case 1:
-        return launch_dtype<D, 1>(ctx, q8, prm, grid, combine);
+        return launch_typed<D, 1>(ctx, prm, grid, combine);
     case 2:
-        return launch_dtype<D, 2>(ctx, q8, prm, grid, combine);
+        return launch_typed<D, 2>(ctx, prm, grid, combine);
     case 3:
-        if constexpr (D <= 128) return launch_dtype<D, 3>(ctx, q8, prm, grid, combine);
+        if constexpr (D <= 128) return launch_typed<D, 3>(ctx, prm, grid, combine);
         break;
     case 4:
-        if constexpr (D <= 128) return launch_dtype<D, 4>(ctx, q8, prm, grid, combine);
+        if constexpr (D <= 128) return launch_typed<D, 4>(ctx, prm, grid, combine);
         break;
     case 8:
-        if constexpr (D <= 64) return launch_dtype<D, 8>(ctx, q8, prm, grid, combine);
+        if constexpr (D <= 64) return launch_typed<D, 8>(ctx, prm, grid, combine);
         break;
     }
     return set_error(GLA_ERR_INVALID, "no decode kernel for head_dim %d and head group %d", D, gt);
@@ -477,7 +404,7 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
     const int group = d.n_heads / d.n_kv_heads;
     const int gt = pick_gt(D, group);
     const int n_hg = (group + gt - 1) / gt;
-    const int ppw = d.q8 ? 2 : 1;  // pages per wave per iteration (NSTEP / 2)
+    const int ppw = kStepsPerIter / 2;  // pages per wave per iteration
 
     // pages a window can span (a start inside a page adds one)
     const int max_pages = d.max_kv_len > 0 ? (d.max_kv_len + GLA_PAGE_SIZE - 1) / GLA_PAGE_SIZE + 1 : 1;
@@ -527,11 +454,11 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
     dim3 grid(max_splits, d.n_kv_heads * n_hg, d.n_seqs);
     switch (D) {
     case 64:
-        return launch_d<64>(ctx, gt, d.q8, prm, grid, max_splits > 1);
+        return launch_d<64>(ctx, gt, prm, grid, max_splits > 1);
     case 128:
-        return launch_d<128>(ctx, gt, d.q8, prm, grid, max_splits > 1);
+        return launch_d<128>(ctx, gt, prm, grid, max_splits > 1);
     case 256:
-        return launch_d<256>(ctx, gt, d.q8, prm, grid, max_splits > 1);
+        return launch_d<256>(ctx, gt, prm, grid, max_splits > 1);
     }
     return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
 }
