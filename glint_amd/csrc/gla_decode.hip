@@ -322,33 +322,92 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
 }
 
 // Log-sum-exp merge of the split partials of one (sequence, kv head, head
-// group).
+// group, q-head g = blockIdx.x). A row of D floats is read by D/4 lanes as
+// float4; the 256 threads form 256/(D/4) split groups that take every
+// NSG-th split, four splits in flight at a time, and are merged through LDS.
 template <int D, int GT>
 __global__ __launch_bounds__(kThreads) void decode_combine_kernel(const DecodeParams p) {
+    constexpr int RL = D / 4;             // lanes per row
+    constexpr int NSG = kThreads / RL;    // split groups
+    constexpr int BATCH = 4;
+    __shared__ float4 lds_a[NSG][RL];
+    __shared__ float lds_m[NSG], lds_l[NSG];
+
     const int b = blockIdx.z;
     const int kvh = blockIdx.y / p.n_hg;
     const int hg = blockIdx.y - kvh * p.n_hg;
-    const int g0 = hg * GT;
-    const int gcount = min(GT, p.group - g0);
-    const int h_base = kvh * p.group + g0;
+    const int g = blockIdx.x;
+    const int gcount = min(GT, p.group - hg * GT);
+    if (g >= gcount) return;
     const SeqRange r = seq_range(p, b);
     if (r.n_splits <= 1) return;
+    const int sg = threadIdx.x / RL;
+    const int e4 = threadIdx.x - sg * RL;
     const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
     const int64_t slot0 = unit * p.max_splits;
-    for (int idx = threadIdx.x; idx < gcount * D; idx += kThreads) {
-        const int g = idx / D;
-        const int e = idx - g * D;
-        float M = -INFINITY;
-        for (int s = 0; s < r.n_splits; s++) M = fmaxf(M, p.part_ml[((slot0 + s) * GT + g) * 2]);
-        float L = 0.0f, A = 0.0f;
-        for (int s = 0; s < r.n_splits; s++) {
-            const float ms = p.part_ml[((slot0 + s) * GT + g) * 2];
-            const float f = (ms == -INFINITY) ? 0.0f : fast_exp2(ms - M);
-            L = fmaf(p.part_ml[((slot0 + s) * GT + g) * 2 + 1], f, L);
-            A = fmaf(p.part_acc[((slot0 + s) * GT + g) * D + e], f, A);
+
+    float M = -INFINITY, L = 0.0f;
+    float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s0 = sg; s0 < r.n_splits; s0 += NSG * BATCH) {
+        float mi[BATCH], li[BATCH];
+        float4 ai[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; j++) {
+            const int s = s0 + j * NSG;
+            const int sc = s < r.n_splits ? s : s0;
+            const int64_t slot = (slot0 + sc) * GT + g;
+            mi[j] = s < r.n_splits ? p.part_ml[slot * 2] : -INFINITY;
+            li[j] = p.part_ml[slot * 2 + 1];
+            ai[j] = reinterpret_cast<const float4 *>(p.part_acc + slot * D)[e4];
         }
-        p.out[((int64_t)b * p.n_heads + h_base + g) * D + e] = L > 0.0f ? A * (1.0f / L) : 0.0f;
+        float bm = M;
+#pragma unroll
+        for (int j = 0; j < BATCH; j++) bm = fmaxf(bm, mi[j]);
+        if (bm == -INFINITY) continue;
+        const float f0 = (M == -INFINITY) ? 0.0f : fast_exp2(M - bm);
+        L *= f0;
+        A.x *= f0;
+        A.y *= f0;
+        A.z *= f0;
+        A.w *= f0;
+#pragma unroll
+        for (int j = 0; j < BATCH; j++) {
+            const float f = (mi[j] == -INFINITY) ? 0.0f : fast_exp2(mi[j] - bm);
+            L = fmaf(li[j], f, L);
+            A.x = fmaf(ai[j].x, f, A.x);
+            A.y = fmaf(ai[j].y, f, A.y);
+            A.z = fmaf(ai[j].z, f, A.z);
+            A.w = fmaf(ai[j].w, f, A.w);
+        }
+        M = bm;
     }
+    lds_a[sg][e4] = A;
+    if (e4 == 0) {
+        lds_m[sg] = M;
+        lds_l[sg] = L;
+    }
+    __syncthreads();
+    if (sg != 0) return;
+    float MM = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NSG; j++) MM = fmaxf(MM, lds_m[j]);
+    float LL = 0.0f;
+    float4 AA = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < NSG; j++) {
+        const float mj = lds_m[j];
+        const float f = (mj == -INFINITY) ? 0.0f : fast_exp2(mj - MM);
+        const float4 aj = lds_a[j][e4];
+        LL = fmaf(lds_l[j], f, LL);
+        AA.x = fmaf(aj.x, f, AA.x);
+        AA.y = fmaf(aj.y, f, AA.y);
+        AA.z = fmaf(aj.z, f, AA.z);
+        AA.w = fmaf(aj.w, f, AA.w);
+    }
+    const float inv = LL > 0.0f ? 1.0f / LL : 0.0f;
+    const int h = kvh * p.group + hg * GT + g;
+    reinterpret_cast<float4 *>(p.out + ((int64_t)b * p.n_heads + h) * D)[e4] =
+        make_float4(AA.x * inv, AA.y * inv, AA.z * inv, AA.w * inv);
 }
 
 template <int D, int GT>
@@ -357,7 +416,7 @@ int launch_typed(gla_ctx *ctx, const DecodeParams &prm, dim3 grid, bool combine)
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "decode_split_kernel launch: %s", hipGetErrorString(e));
     if (combine) {
-        hipLaunchKernelGGL((decode_combine_kernel<D, GT>), dim3(1, grid.y, grid.z), dim3(kThreads), 0, ctx->stream,
+        hipLaunchKernelGGL((decode_combine_kernel<D, GT>), dim3(GT, grid.y, grid.z), dim3(kThreads), 0, ctx->stream,
                            prm);
         e = hipGetLastError();
         if (e != hipSuccess)
