@@ -101,6 +101,13 @@ __device__ __forceinline__ SeqRange seq_range(const DecodeParams &p, int b) {
     return r;
 }
 
+// 16-byte non-temporal load: K/V bytes are read once per call.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_nt(const uint8_t *p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float word_f(const uint4 &c, int w) {
     return __uint_as_float(w == 0 ? c.x : (w == 1 ? c.y : (w == 2 ? c.z : c.w)));
 }
@@ -116,10 +123,12 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
     __shared__ float lds_m[kWaves][GT];
     __shared__ float lds_l[kWaves][GT];
 
-    const int split = blockIdx.x;
+    // grid (KV head x head group, split, sequence): head index fastest, so
+    // the head spans of the same pages are read together
+    const int split = blockIdx.y;
     const int b = blockIdx.z;
-    const int kvh = blockIdx.y / p.n_hg;
-    const int hg = blockIdx.y - kvh * p.n_hg;
+    const int kvh = blockIdx.x / p.n_hg;
+    const int hg = blockIdx.x - kvh * p.n_hg;
     const int g0 = hg * GT;
     const int gcount = min(GT, p.group - g0);
     const int h_base = kvh * p.group + g0;
@@ -183,8 +192,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
             const uint8_t *vp = p.kv.v + base;
 #pragma unroll
             for (int i = 0; i < NCH; i++) {
-                kr[s][i] = *reinterpret_cast<const uint4 *>(kp + (i * 8 + sub) * 16);
-                vr[s][i] = *reinterpret_cast<const uint4 *>(vp + (i * 8 + sub) * 16);
+                kr[s][i] = load_nt(kp + (i * 8 + sub) * 16);
+                vr[s][i] = load_nt(vp + (i * 8 + sub) * 16);
             }
         }
 
@@ -416,7 +425,7 @@ int launch_typed(gla_ctx *ctx, const DecodeParams &prm, dim3 grid, bool combine)
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "decode_split_kernel launch: %s", hipGetErrorString(e));
     if (combine) {
-        hipLaunchKernelGGL((decode_combine_kernel<D, GT>), dim3(GT, grid.y, grid.z), dim3(kThreads), 0, ctx->stream,
+        hipLaunchKernelGGL((decode_combine_kernel<D, GT>), dim3(GT, grid.x, grid.z), dim3(kThreads), 0, ctx->stream,
                            prm);
         e = hipGetLastError();
         if (e != hipSuccess)
@@ -510,7 +519,8 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
         prm.part_ml = (float *)((uint8_t *)ctx->scratch + acc_b);
     }
     if (d.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "decode: n_seqs %d > 65535", d.n_seqs);
-    dim3 grid(max_splits, d.n_kv_heads * n_hg, d.n_seqs);
+    if (max_splits > 65535) return set_error(GLA_ERR_INVALID, "decode: %d splits per sequence > 65535", max_splits);
+    dim3 grid(d.n_kv_heads * n_hg, max_splits, d.n_seqs);
     switch (D) {
     case 64:
         return launch_d<64>(ctx, gt, prm, grid, max_splits > 1);

@@ -180,43 +180,56 @@ __device__ __forceinline__ int pow2_exp(float x) {
     return e < -100 ? -100 : (e > 100 ? 100 : e);
 }
 
-// The lane's operands of one step, in registers.
+// The lane's operands of one step, in registers: the K half is read at the
+// top of the step and the V half after the softmax, so only one half is live
+// at a time.
 template <int D>
-struct Raw {
-    static constexpr int NQ = D / 64;  // uint4 per lane per (page, head) K or V block
+struct RawK {
+    static constexpr int NQ = D / 64;  // uint4 per lane per (page, head) K block
     static constexpr int NB = D / 32;
     uint4 k[2][NQ];
+    uint32_t ks[2][NB];  // 4 positions x the lane's NB/2 blocks, per page
+};
+template <int D>
+struct RawV {
+    static constexpr int NQ = D / 64;
+    static constexpr int NB = D / 32;
     uint4 v[2][NQ];
-    uint32_t ks[2][NB];   // 4 positions x the lane's NB/2 blocks, per page
     uint32_t vs[2 * NB];  // 4 positions x NB blocks, the lane's P.V page only
 };
 
 // ---- the LDS slot: direct global -> LDS loads (gfx950 global_load_lds) ----
 //
-// Each wave streams its chunk through one LDS slot of two pages:
-// K_a | K_b | V_a | V_b (16*D bytes each, byte copies of the (page, head)
-// quant blocks: lane l's piece c at c*1024 + l*16) and the scales Ks_a | Ks_b | Vs_a | Vs_b (D bytes each). At
-// the top of a step the wave copies the slot into registers and refills it
-// with the next step, which is then in flight while this step computes.
+// Each wave streams its chunk through one LDS slot of two pages, in two
+// halves: K = K_a | K_b | Ks_a | Ks_b and V = V_a | V_b | Vs_a | Vs_b (16*D
+// bytes per quant block, byte copies of the (page, head) blocks with lane l's
+// piece c at c*1024 + l*16; D bytes per scale array). At the top of a step
+// the wave copies the K half into registers and refills it with the next
+// step; after the softmax it does the same with the V half. Each half's next
+// step is in flight for a whole step, and only one half is held in
+// registers at a time.
 // The loads are issued from inline assembly with explicit vmcnt waits: the
 // compiler's own wait insertion would wait for every outstanding LDS load
 // before any LDS read. Every vector-memory instruction of the streaming loop
 // is one of these, so the counts are exact; the compiler's waits for its own
 // earlier loads stay correct because extra outstanding loads only make an
 // in-order wait wait longer.
-constexpr int kSlotBytesPerD = 68;  // 64*D quant bytes + 4*D scale bytes per step
+constexpr int kSlotBytesPerD = 68;  // per half: 32*D quant bytes + 2*D scale bytes
+constexpr int kHalfV = 34;         // the V half starts at 34*D
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
 // 16 bytes per lane from g into LDS at m0 + 16*lane (m0 restored afterwards).
+// The loads are non-temporal (nt): every byte is read once per call, and
+// streaming them past the caches measured ~10% faster than default loads.
 __device__ __forceinline__ void dma16(const void *g, uint32_t m0) {
     uint32_t save;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %2\n\t"
-        "global_load_lds_dwordx4 %1, off\n\t"
+        "global_load_lds_dwordx4 %1, off nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(save)
         : "v"(g), "s"(m0)
@@ -229,7 +242,7 @@ __device__ __forceinline__ void dma4(const void *g, uint32_t m0) {
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %2\n\t"
-        "global_load_lds_dword %1, off\n\t"
+        "global_load_lds_dword %1, off nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(save)
         : "v"(g), "s"(m0)
@@ -237,35 +250,46 @@ __device__ __forceinline__ void dma4(const void *g, uint32_t m0) {
 }
 
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N vector-memory loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Issue the loads of step `step` (pages 2*step, 2*step+1 of the chunk) into
-// the slot at LDS byte address `slot`.
+// Loads per half-step: the two quant blocks in kilobyte pieces and the two
+// scale arrays in 256-byte dword loads.
 template <int D>
-__device__ __forceinline__ void issue_step(const Q8Params &p, const uint8_t *head_base, int pid_l, int step,
+constexpr int kLoadsPerHalf = 2 * (D / 64) + (2 * D + 255) / 256;
+
+// Issue the loads of half V (0: K, 1: V) of step `step` (pages 2*step,
+// 2*step+1 of the chunk) into the slot at LDS byte address `slot`.
+template <int D, int V>
+__device__ __forceinline__ void issue_half(const Q8Params &p, const uint8_t *head_base, int pid_l, int step,
                                            int npg, int lane, uint32_t slot) {
     constexpr int NQ = D / 64;
     const int pa = 2 * step;
     const int pb = (pa + 1 < npg) ? pa + 1 : pa;
     const int ida = __builtin_amdgcn_readlane(pid_l, pa);
     const int idb = __builtin_amdgcn_readlane(pid_l, pb);
-    const uint8_t *ba = head_base + (int64_t)ida * p.page_stride;
-    const uint8_t *bb = head_base + (int64_t)idb * p.page_stride;
+    const uint8_t *ba = head_base + (int64_t)ida * p.page_stride + V * 16 * D;
+    const uint8_t *bb = head_base + (int64_t)idb * p.page_stride + V * 16 * D;
+    const uint32_t dst = slot + V * kHalfV * D;
     // byte copies of the quant blocks, one contiguous kilobyte per load
 #pragma unroll
     for (int c = 0; c < NQ; c++) {
-        dma16(ba + c * 1024 + lane * 16, slot + 0 * 16 * D + c * 1024);
-        dma16(bb + c * 1024 + lane * 16, slot + 1 * 16 * D + c * 1024);
-        dma16(ba + 16 * D + c * 1024 + lane * 16, slot + 2 * 16 * D + c * 1024);
-        dma16(bb + 16 * D + c * 1024 + lane * 16, slot + 3 * 16 * D + c * 1024);
+        dma16(ba + c * 1024 + lane * 16, dst + c * 1024);
+        dma16(bb + c * 1024 + lane * 16, dst + 16 * D + c * 1024);
     }
-    // scales, byte-identical: [Ks_a | Ks_b | Vs_a | Vs_b], 256 bytes per load
+    // scales, byte-identical: [s_a | s_b] from 32*D (K) or 33*D (V) of the
+    // page-head; at D = 64 the upper half of the wave idles
+    const uint8_t *sa = head_base + (int64_t)ida * p.page_stride + (32 + V) * D;
+    const uint8_t *sb = head_base + (int64_t)idb * p.page_stride + (32 + V) * D;
 #pragma unroll
-    for (int j = 0; j < D / 64; j++) {
+    for (int j = 0; j < (2 * D + 255) / 256; j++) {
         const int i = j * 256 + lane * 4;
-        const int reg = i / D;  // 0 Ks_a, 1 Ks_b, 2 Vs_a, 3 Vs_b
-        const uint8_t *src = ((reg & 1) ? bb : ba) + (reg < 2 ? 32 * D : 33 * D) + (i - reg * D);
-        dma4(src, slot + 64 * D + j * 256);
+        if (i < 2 * D) dma4((i < D ? sa : sb) + (i < D ? i : i - D), dst + 32 * D + j * 256);
     }
 }
 
@@ -291,26 +315,37 @@ __device__ __forceinline__ void lds_words(const uint8_t *src, uint32_t (&dst)[N]
     }
 }
 
-// Copy the lane's operands of a landed step from the slot.
+// Copy the lane's operands of a landed half-step from the slot.
 template <int D>
-__device__ __forceinline__ void read_step(const uint8_t *slot, int lane, Raw<D> &r) {
+__device__ __forceinline__ void read_k(const uint8_t *slot, int lane, RawK<D> &r) {
     constexpr int NQ = D / 64;
     constexpr int NB = D / 32;
     const int kg = lane >> 4;
-    const int hb = (lane >> 3) & 1;  // the lane's block parity (S) / page (P'.V)
+    const int hb = (lane >> 3) & 1;  // the lane's block parity
 #pragma unroll
     for (int c = 0; c < NQ; c++) {
         r.k[0][c] = *reinterpret_cast<const uint4 *>(slot + 0 * 16 * D + c * 1024 + lane * 16);
         r.k[1][c] = *reinterpret_cast<const uint4 *>(slot + 1 * 16 * D + c * 1024 + lane * 16);
-        r.v[0][c] = *reinterpret_cast<const uint4 *>(slot + 2 * 16 * D + c * 1024 + lane * 16);
-        r.v[1][c] = *reinterpret_cast<const uint4 *>(slot + 3 * 16 * D + c * 1024 + lane * 16);
     }
     // K scales: [parity][slot][NB/2] f16; the lane's 4 positions of its parity
-    const uint8_t *ks = slot + 64 * D + (hb * 16 + kg * 4) * NB;
+    const uint8_t *ks = slot + 32 * D + (hb * 16 + kg * 4) * NB;
     lds_words(ks, r.ks[0]);
     lds_words(ks + D, r.ks[1]);
+}
+template <int D>
+__device__ __forceinline__ void read_v(const uint8_t *slot, int lane, RawV<D> &r) {
+    constexpr int NQ = D / 64;
+    constexpr int NB = D / 32;
+    const int kg = lane >> 4;
+    const int hb = (lane >> 3) & 1;  // the lane's P'.V page
+    const uint8_t *vh = slot + kHalfV * D;
+#pragma unroll
+    for (int c = 0; c < NQ; c++) {
+        r.v[0][c] = *reinterpret_cast<const uint4 *>(vh + 0 * 16 * D + c * 1024 + lane * 16);
+        r.v[1][c] = *reinterpret_cast<const uint4 *>(vh + 1 * 16 * D + c * 1024 + lane * 16);
+    }
     // V scales: [slot][NB] f16; the lane's 4 positions of its page
-    lds_words(slot + 64 * D + (2 + hb) * D + kg * 4 * NB * 2, r.vs);
+    lds_words(vh + 32 * D + hb * D + kg * 4 * NB * 2, r.vs);
 }
 
 template <int D>
@@ -330,9 +365,13 @@ struct StepState {
     float lsum;  // sum of p over this lane's P' positions
 };
 
-// One step: two pages (32 positions) of one (sequence, KV head).
+// First half of a step (two pages, 32 positions, of one sequence and KV
+// head): S = K.Q, the soft-cap, the window mask and the online softmax.
+// Leaves in pr the probabilities of the lane's four P' positions and in
+// vbad the positions whose V scale must be ignored (bit i).
 template <int D>
-__device__ __forceinline__ void step_body(Raw<D> &cur, int step, const StepConst<D> &c, StepState<D> &st) {
+__device__ __forceinline__ void step_qk(const RawK<D> &cur, int step, const StepConst<D> &c, StepState<D> &st,
+                                        float (&pr)[4], int &vbad) {
     constexpr int NB = D / 32;
     constexpr int ND = D / 16;
 
@@ -374,8 +413,9 @@ __device__ __forceinline__ void step_body(Raw<D> &cur, int step, const StepConst
 
     // Window / length mask: only a chunk's first and last steps can hold
     // positions outside [start, end). Masked positions get score -inf and,
-    // on the lane's own page, a zero V scale, so a non-finite scale of an
-    // unused position cannot reach the output.
+    // on the lane's own page, are flagged so that their V scale is zeroed and
+    // a non-finite scale of an unused position cannot reach the output.
+    vbad = 0;
     const int sp = (c.pg0 + 2 * step) * 16;             // first position of the step
     const int lim1 = min(c.end, (c.pg0 + c.npg) * 16);  // page 1 of the step may be past the chunk
     if (sp < c.start || sp + 32 > lim1) {
@@ -387,8 +427,7 @@ __device__ __forceinline__ void step_body(Raw<D> &cur, int step, const StepConst
             s0[i] = ok0 ? s0[i] : -INFINITY;
             s1[i] = ok1 ? s1[i] : -INFINITY;
             const bool ok = c.ph ? ok1 : ok0;
-#pragma unroll
-            for (int w = 0; w < NB / 2; w++) cur.vs[i * (NB / 2) + w] = ok ? cur.vs[i * (NB / 2) + w] : 0u;
+            vbad |= ok ? 0 : (1 << i);
         }
     }
     const float tmax = max_rows(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
@@ -397,7 +436,6 @@ __device__ __forceinline__ void step_body(Raw<D> &cur, int step, const StepConst
     const float alpha = fast_exp2(st.m - m_new);
     st.m = m_new;
 
-    float pr[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) pr[i] = fast_exp2((c.ph ? s1[i] : s0[i]) - m_new);
     st.lsum = st.lsum * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
@@ -414,9 +452,21 @@ __device__ __forceinline__ void step_body(Raw<D> &cur, int step, const StepConst
             st.acc[t][3] *= aB;
         }
     }
+}
 
-    // O += P' . V, one 32-element block (two d tiles) at a time.
-    // v = p * vscale * 2^kv; the lane's piece is f16(v - pf * f16(v)).
+// Second half of a step: O += P' . V, one 32-element block (two d tiles) at
+// a time. v = p * vscale * 2^kv; the lane's piece is f16(v - pf * f16(v)).
+template <int D>
+__device__ __forceinline__ void step_pv(RawV<D> &cur, const StepConst<D> &c, StepState<D> &st, const float (&pr)[4],
+                                        int vbad) {
+    constexpr int NB = D / 32;
+    if (vbad) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int w = 0; w < NB / 2; w++)
+                cur.vs[i * (NB / 2) + w] = ((vbad >> i) & 1) ? 0u : cur.vs[i * (NB / 2) + w];
+    }
     float pv[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) pv[i] = pr[i] * c.vsc;
@@ -477,10 +527,6 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
     const int pid_l = (int)map_page(p.pm, b, pg0 + min(lane, npg - 1));
     const uint8_t *head_base = p.base + (int64_t)kvh * p.head_stride;
 
-    // start streaming the first step; the q split and the V-scale scan overlap it
-    const uint32_t slot_lds = __builtin_amdgcn_readfirstlane(lds_addr(slot));
-    issue_step<D>(p, head_base, pid_l, 0, npg, lane, slot_lds);
-
     // ---- Q as the B operand of S = K.Q ----
     float qx[NB][8];
     float qmax = 0.0f;
@@ -511,19 +557,31 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
         }
     c.inv_qs = ldexpf(1.0f, qe - 14);
 
+    // start streaming the first step; the V-scale scan overlaps it. (The
+    // q split above comes first: the compiler does not count these loads, so
+    // a wait it placed for q after them would wait for them as well.)
+    const uint32_t slot_lds = __builtin_amdgcn_readfirstlane(lds_addr(slot));
+    issue_half<D, 0>(p, head_base, pid_l, 0, npg, lane, slot_lds);
+    issue_half<D, 1>(p, head_base, pid_l, 0, npg, lane, slot_lds);
+
     // ---- largest V scale of the chunk: P' = p * vscale * 2^kv stays below 2^14 ----
     float inv_vsc;
     {
         float vmax = 0.0f;
         const int units = npg * 2 * NB;  // 16-byte units of the chunk's V scales
-        for (int u0 = 0; u0 < units; u0 += 64) {
-            const int u = u0 + lane;
-            const int uu = min(u, units - 1);
-            const int pid = __shfl(pid_l, uu / (2 * NB));
-            if (u < units) {
-                const uint4 w = *reinterpret_cast<const uint4 *>(head_base + (int64_t)pid * p.page_stride + 33 * D +
-                                                                 (uu % (2 * NB)) * 16);
-                const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+        // four loads per lane in flight per batch (one batch up to 128 pages at d128)
+        for (int u0 = 0; u0 < units; u0 += 256) {
+            uint4 w[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int uu = min(u0 + j * 64 + lane, units - 1);
+                const int pid = __shfl(pid_l, uu / (2 * NB));
+                w[j] = *reinterpret_cast<const uint4 *>(head_base + (int64_t)pid * p.page_stride + 33 * D +
+                                                        (uu % (2 * NB)) * 16);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t a[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
 #pragma unroll
                 for (int i = 0; i < 8; i++) vmax = fmaxf(vmax, fabsf(half_at(a, i)));
             }
@@ -551,15 +609,31 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
     st.m = -INFINITY;
     st.lsum = 0.0f;
 
+    constexpr int NL = kLoadsPerHalf<D>;
     for (int step = 0; step < nsteps; step++) {
-        wait_vmem_all();  // step `step` has landed
-        Raw<D> cur;
-        read_step<D>(slot, lane, cur);
-        if (step + 1 < nsteps) {
-            wait_lds();  // the slot is copied: refill it with the next step
-            issue_step<D>(p, head_base, pid_l, step + 1, npg, lane, slot_lds);
+        const bool next = step + 1 < nsteps;
+        wait_vmem<NL>();  // the K half of `step` has landed (its V half may not have)
+        RawK<D> kr;
+        read_k<D>(slot, lane, kr);
+        if (next) {
+            wait_lds();  // the K half is copied: refill it with the next step
+            issue_half<D, 0>(p, head_base, pid_l, step + 1, npg, lane, slot_lds);
         }
-        step_body<D>(cur, step, c, st);
+        float pr[4];
+        int vbad;
+        step_qk<D>(kr, step, c, st, pr, vbad);
+        // the V half of `step` has landed; only the next K half may be in flight
+        if (next)
+            wait_vmem<NL>();
+        else
+            wait_vmem<0>();
+        RawV<D> vr;
+        read_v<D>(slot, lane, vr);
+        if (next) {
+            wait_lds();
+            issue_half<D, 1>(p, head_base, pid_l, step + 1, npg, lane, slot_lds);
+        }
+        step_pv<D>(vr, c, st, pr, vbad);
     }
     wait_vmem_all();
 
@@ -610,9 +684,13 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    // grid (KV head x head group, workgroup of the sequence, sequence): the
+    // head index runs fastest, so the workgroups reading the 8 head spans of
+    // the same pages are dispatched together and the DRAM rows those pages
+    // open are read out while open (measured ~25% over chunk-fastest order)
     const int b = blockIdx.z;
-    const int kvh = blockIdx.y / p.n_hg;
-    const int hg = blockIdx.y - kvh * p.n_hg;
+    const int kvh = blockIdx.x / p.n_hg;
+    const int hg = blockIdx.x - kvh * p.n_hg;
     const int g0 = hg * kGT;
     const int gcount = min(kGT, p.group - g0);
     const int h_base = kvh * p.group + g0;
@@ -620,13 +698,13 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
 
     const Range r = seq_range(p, b);
     if (r.n_pages == 0) {  // empty window: zero output (the reference's pre-zeroed buffer)
-        if (blockIdx.x == 0)
+        if (blockIdx.y == 0)
             for (int idx = tid; idx < gcount * D; idx += kThreads) out[idx] = 0.0f;
         return;
     }
     const int n_chunks = (r.n_pages + p.ch - 1) / p.ch;
     const int n_wg = (n_chunks + kWaves - 1) / kWaves;
-    const int wg = blockIdx.x;
+    const int wg = blockIdx.y;
     if (wg >= n_wg) return;
     const int chunk = wg * kWaves + wave;
     if (chunk < n_chunks) {
@@ -734,7 +812,7 @@ int launch_d(gla_ctx *ctx, const Q8Params &prm, dim3 grid) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "decode_q8_mfma_kernel launch: %s", hipGetErrorString(e));
     if (prm.max_wg > 1) {
-        hipLaunchKernelGGL((decode_q8_combine_kernel<D>), dim3(kGT * D / 256, grid.y, grid.z), dim3(256), 0,
+        hipLaunchKernelGGL((decode_q8_combine_kernel<D>), dim3(kGT * D / 256, grid.x, grid.z), dim3(256), 0,
                            ctx->stream, prm);
         e = hipGetLastError();
         if (e != hipSuccess)
@@ -793,7 +871,8 @@ int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
         prm.part = (float *)ctx->scratch;
     }
     if (d.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "decode: n_seqs %d > 65535", d.n_seqs);
-    dim3 grid((unsigned)max_wg, d.n_kv_heads * n_hg, d.n_seqs);
+    if (max_wg > 65535) return set_error(GLA_ERR_INVALID, "decode: %lld workgroups per sequence > 65535", (long long)max_wg);
+    dim3 grid(d.n_kv_heads * n_hg, (unsigned)max_wg, d.n_seqs);
     switch (D) {
     case 64:
         return launch_d<64>(ctx, prm, grid);
