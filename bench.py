@@ -176,6 +176,7 @@ class PagedDecode:
             self.layers.append(dict(
                 pb=pb, q=be.buffer(q), q_host=q, out=be.empty(q.nbytes),
                 start=be.buffer(pb.kv_start), len=be.buffer(pb.kv_len), table=be.buffer(table),
+                start_host=np.ascontiguousarray(pb.kv_start, np.int32), len_host=np.ascontiguousarray(pb.kv_len, np.int32),
                 stride=table.shape[1], max_len=int(pb.kv_len.max()),
                 bytes=uniq * tok + pages_read(pb) * 4 + 2 * q.nbytes,
                 bytes_logical=logical * tok + pages_read(pb) * 4 + 2 * q.nbytes,
@@ -185,8 +186,11 @@ class PagedDecode:
 
     def step(self, i):
         L = self.layers[i % self.n_layers]
+        # the engine keeps every sequence's position on the host and passes the
+        # host copies along (they size the launch; see gla_decode_args)
         self.be.decode(self.pool, L["q"], L["out"], L["start"], L["len"], len(self.ctx), L["max_len"], self.H,
-                       self.scale, self.softcap, page_table=L["table"], page_table_stride=L["stride"])
+                       self.scale, self.softcap, page_table=L["table"], page_table_stride=L["stride"],
+                       kv_start_host=L["start_host"], kv_len_host=L["len_host"])
 
     def bytes_per_step(self):
         return float(np.mean([L["bytes"] for L in self.layers]))

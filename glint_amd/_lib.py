@@ -62,6 +62,8 @@ class DecodeArgs(C.Structure):
         ("softcap", C.c_float),
         ("q", C.c_void_p),
         ("out", C.c_void_p),
+        ("kv_start_host", C.c_void_p),
+        ("kv_len_host", C.c_void_p),
     ]
 
 

@@ -284,8 +284,11 @@ class GpuBackend:
     def decode(self, kv: _KvBase, q: DeviceBuffer, out: DeviceBuffer, kv_start: DeviceBuffer,
                kv_len: DeviceBuffer, n_seqs: int, max_kv_len: int, n_heads: int, scale: float,
                softcap: Optional[float] = None, layer: int = 0, seq_slot: Optional[DeviceBuffer] = None,
-               page_table: Optional[DeviceBuffer] = None, page_table_stride: int = 0) -> None:
-        """gla_decode on device buffers (asynchronous on the backend's stream)."""
+               page_table: Optional[DeviceBuffer] = None, page_table_stride: int = 0,
+               kv_start_host: Optional[np.ndarray] = None, kv_len_host: Optional[np.ndarray] = None) -> None:
+        """gla_decode on device buffers (asynchronous on the backend's stream). kv_start_host /
+        kv_len_host: optional host copies of the device arrays (int32[B]); they let the library
+        size the launch to the real lengths."""
         a = _lib.DecodeArgs()
         a.kv = kv.handle
         a.layer = layer
@@ -301,6 +304,15 @@ class GpuBackend:
         a.softcap = _cap(softcap)
         a.q = q.ptr
         a.out = out.ptr
+        if (kv_start_host is None) != (kv_len_host is None):
+            raise ValueError("pass both kv_start_host and kv_len_host, or neither")
+        if kv_start_host is not None:
+            hs = np.ascontiguousarray(kv_start_host, dtype=np.int32)
+            hl = np.ascontiguousarray(kv_len_host, dtype=np.int32)
+            if hs.shape != (n_seqs,) or hl.shape != (n_seqs,):
+                raise ValueError("kv_start_host / kv_len_host must be int32[n_seqs]")
+            a.kv_start_host = hs.ctypes.data
+            a.kv_len_host = hl.ctypes.data
         check(_lib.lib().gla_decode(self.ctx, C.byref(a)))
 
     def prefill(self, kv: _KvBase, q: DeviceBuffer, out: DeviceBuffer, q_start: DeviceBuffer,

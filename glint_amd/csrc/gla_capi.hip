@@ -498,6 +498,10 @@ int gla_decode(gla_ctx *ctx, const gla_decode_args *a) {
     d.softcap = a->softcap;
     d.q = a->q;
     d.out = a->out;
+    GLA_REQUIRE((a->kv_start_host == nullptr) == (a->kv_len_host == nullptr),
+                "gla_decode: pass both kv_start_host and kv_len_host, or neither");
+    d.kv_start_host = a->kv_start_host;
+    d.kv_len_host = a->kv_len_host;
     GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
     return launch_decode(ctx, d);
     GLA_GUARD_END

@@ -43,6 +43,8 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <cmath>
+#include <vector>
 
 #include "gla_internal.h"
 
@@ -221,31 +223,40 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
-// 16 bytes per lane from g into LDS at m0 + 16*lane (m0 restored afterwards).
+// 16 bytes per lane from sbase + voff into LDS at m0 + 16*lane (m0 restored
+// afterwards); sbase is wave-uniform (SGPRs), so the per-load address needs
+// no 64-bit arithmetic on the VALU.
 // The loads are non-temporal (nt): every byte is read once per call, and
 // streaming them past the caches measured ~10% faster than default loads.
-__device__ __forceinline__ void dma16(const void *g, uint32_t m0) {
+__device__ __forceinline__ void dma16_s(const uint8_t *sbase, uint32_t voff, uint32_t m0) {
     uint32_t save;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "global_load_lds_dwordx4 %1, off nt\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %2 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(save)
-        : "v"(g), "s"(m0)
+        : "v"(voff), "s"(sbase), "s"(m0)
         : "memory");
 }
 
-// 4 bytes per lane from g into LDS at m0 + 4*lane.
-__device__ __forceinline__ void dma4(const void *g, uint32_t m0) {
-    uint32_t save;
+// 4 bytes per lane from sbase + voff into LDS at m0 + 4*lane, for the lanes
+// of the 64-bit mask (mlo | mhi << 32) only; exec is restored afterwards.
+__device__ __forceinline__ void dma4_s(const uint8_t *sbase, uint32_t voff, uint32_t m0, uint32_t mlo,
+                                       uint32_t mhi) {
+    uint64_t save_exec;
+    uint32_t save_m0;
     asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "global_load_lds_dword %1, off nt\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(save)
-        : "v"(g), "s"(m0)
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b32 exec_lo, %4\n\t"
+        "s_mov_b32 exec_hi, %5\n\t"
+        "s_mov_b32 %1, m0\n\t"
+        "s_mov_b32 m0, %6\n\t"
+        "global_load_lds_dword %2, %3 nt\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(save_exec), "=&s"(save_m0)
+        : "v"(voff), "s"(sbase), "s"(mlo), "s"(mhi), "s"(m0)
         : "memory");
 }
 
@@ -258,10 +269,10 @@ __device__ __forceinline__ void wait_vmem() {
 }
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Loads per half-step: the two quant blocks in kilobyte pieces and the two
-// scale arrays in 256-byte dword loads.
+// Loads per half-step: the two quant blocks in kilobyte pieces and one
+// dword load per scale array.
 template <int D>
-constexpr int kLoadsPerHalf = 2 * (D / 64) + (2 * D + 255) / 256;
+constexpr int kLoadsPerHalf = 2 * (D / 64) + 2;
 
 // Issue the loads of half V (0: K, 1: V) of step `step` (pages 2*step,
 // 2*step+1 of the chunk) into the slot at LDS byte address `slot`.
@@ -277,19 +288,28 @@ __device__ __forceinline__ void issue_half(const Q8Params &p, const uint8_t *hea
     const uint8_t *bb = head_base + (int64_t)idb * p.page_stride + V * 16 * D;
     const uint32_t dst = slot + V * kHalfV * D;
     // byte copies of the quant blocks, one contiguous kilobyte per load
+    const uint32_t voff = (uint32_t)lane * 16;
 #pragma unroll
     for (int c = 0; c < NQ; c++) {
-        dma16(ba + c * 1024 + lane * 16, dst + c * 1024);
-        dma16(bb + c * 1024 + lane * 16, dst + 16 * D + c * 1024);
+        dma16_s(ba + c * 1024, voff, dst + c * 1024);
+        dma16_s(bb + c * 1024, voff, dst + 16 * D + c * 1024);
     }
     // scales, byte-identical: [s_a | s_b] from 32*D (K) or 33*D (V) of the
-    // page-head; at D = 64 the upper half of the wave idles
+    // page-head, D bytes each = D/4 lanes of one dword. Up to d128 both fit
+    // one wave-wide LDS row and go out as two lane-masked loads sharing m0.
     const uint8_t *sa = head_base + (int64_t)ida * p.page_stride + (32 + V) * D;
     const uint8_t *sb = head_base + (int64_t)idb * p.page_stride + (32 + V) * D;
-#pragma unroll
-    for (int j = 0; j < (2 * D + 255) / 256; j++) {
-        const int i = j * 256 + lane * 4;
-        if (i < 2 * D) dma4((i < D ? sa : sb) + (i < D ? i : i - D), dst + 32 * D + j * 256);
+    const uint32_t voff4 = (uint32_t)lane * 4;
+    if constexpr (D == 256) {
+        dma4_s(sa, voff4, dst + 32 * D, 0xffffffffu, 0xffffffffu);
+        dma4_s(sb, voff4, dst + 32 * D + 256, 0xffffffffu, 0xffffffffu);
+    } else if constexpr (D == 128) {
+        dma4_s(sa, voff4, dst + 32 * D, 0xffffffffu, 0u);
+        dma4_s(sb - D, voff4, dst + 32 * D, 0u, 0xffffffffu);
+    } else {
+        static_assert(D == 64, "head_dim 64, 128 or 256");
+        dma4_s(sa, voff4, dst + 32 * D, 0x0000ffffu, 0u);
+        dma4_s(sb - D, voff4, dst + 32 * D, 0xffff0000u, 0u);
     }
 }
 
@@ -351,7 +371,10 @@ __device__ __forceinline__ void read_v(const uint8_t *slot, int lane, RawV<D> &r
 template <int D>
 struct StepConst {
     half8 qb[D / 32];  // Q operand per block (zero unless the block's parity is the lane's)
-    float inv_qs, vsc, softcap, inv_cap;
+    // Scores are kept in the q-scaled domain: the log2-domain score is
+    // sm * s (sm = 2^(qe - 14), or 1 after a soft-cap, which is applied to
+    // the true score). P' is p * 2^kvs * vscale, 2^kvs folded into the exp.
+    float sm, kvs, softcap, qcap;
     bool cap;
     int pg0, npg, start, end;
     int kg, ph;
@@ -394,7 +417,6 @@ __device__ __forceinline__ void step_qk(const RawK<D> &cur, int step, const Step
             float x = 0.0f;
 #pragma unroll
             for (int j = 0; j < NB / 2; j++) x = fmaf(half_at(cur.ks[P], i * (NB / 2) + j), cp[j][i], x);
-            x *= c.inv_qs;
             x += dpp_ror8(x);   // even blocks + odd blocks
             x += dpp_swap1(x);  // hi piece + lo piece
             if (P == 0)
@@ -406,8 +428,8 @@ __device__ __forceinline__ void step_qk(const RawK<D> &cur, int step, const Step
     if (c.cap) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            s0[i] = c.softcap * tanh_approx(s0[i] * c.inv_cap) * kLog2e;
-            s1[i] = c.softcap * tanh_approx(s1[i] * c.inv_cap) * kLog2e;
+            s0[i] = c.softcap * tanh_approx(s0[i] * c.qcap) * kLog2e;
+            s1[i] = c.softcap * tanh_approx(s1[i] * c.qcap) * kLog2e;
         }
     }
 
@@ -433,11 +455,12 @@ __device__ __forceinline__ void step_qk(const RawK<D> &cur, int step, const Step
     const float tmax = max_rows(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
                                       fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))));
     const float m_new = fmaxf(st.m, tmax);  // finite: page 0 of a step always holds a position
-    const float alpha = fast_exp2(st.m - m_new);
+    const float alpha = fast_exp2((st.m - m_new) * c.sm);
     st.m = m_new;
+    const float off = c.kvs - m_new * c.sm;
 
 #pragma unroll
-    for (int i = 0; i < 4; i++) pr[i] = fast_exp2((c.ph ? s1[i] : s0[i]) - m_new);
+    for (int i = 0; i < 4; i++) pr[i] = fast_exp2(fmaf(c.ph ? s1[i] : s0[i], c.sm, off));
     st.lsum = st.lsum * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
 
     if (__ballot(alpha != 1.0f)) {
@@ -467,14 +490,11 @@ __device__ __forceinline__ void step_pv(RawV<D> &cur, const StepConst<D> &c, Ste
             for (int w = 0; w < NB / 2; w++)
                 cur.vs[i * (NB / 2) + w] = ((vbad >> i) & 1) ? 0u : cur.vs[i * (NB / 2) + w];
     }
-    float pv[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) pv[i] = pr[i] * c.vsc;
 #pragma unroll
     for (int blk = 0; blk < NB; blk++) {
         float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = pv[i] * half_at(cur.vs, i * NB + blk);
+        for (int i = 0; i < 4; i++) v[i] = fmaf(pr[i], half_at(cur.vs, i * NB + blk), 0.0f);
         const half2v h01 = __builtin_convertvector((float2v){v[0], v[1]}, half2v);
         const half2v h23 = __builtin_convertvector((float2v){v[2], v[3]}, half2v);
         const half2v e01 = {(_Float16)fmaf(-c.pf, (float)h01[0], v[0]), (_Float16)fmaf(-c.pf, (float)h01[1], v[1])};
@@ -555,7 +575,7 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
             const bool mine = qvalid && ((blk & 1) == ph);
             c.qb[blk][s] = mine ? (piece ? lo : hi) : (_Float16)0.0f;
         }
-    c.inv_qs = ldexpf(1.0f, qe - 14);
+    const float inv_qs = ldexpf(1.0f, qe - 14);
 
     // start streaming the first step; the V-scale scan overlaps it. (The
     // q split above comes first: the compiler does not count these loads, so
@@ -588,13 +608,14 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
         }
         vmax = wave_max(vmax);
         const int ve = pow2_exp(vmax);
-        c.vsc = ldexpf(1.0f, 14 - ve);
+        c.kvs = (float)(14 - ve);
         inv_vsc = ldexpf(1.0f, ve - 14);
     }
 
     c.cap = p.softcap > 0.0f;
     c.softcap = p.softcap;
-    c.inv_cap = c.cap ? 1.0f / p.softcap : 0.0f;
+    c.qcap = c.cap ? inv_qs / p.softcap : 0.0f;
+    c.sm = c.cap ? 1.0f : inv_qs;
     c.pg0 = pg0;
     c.npg = npg;
     c.start = r.start;
@@ -639,7 +660,7 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
 
     // ---- per-head totals ----
     // l of head gq: add the two pages (lane ^ 8) and the four lane groups
-    const float L = sum_rows(st.lsum + dpp_ror8(st.lsum));
+    const float L = sum_rows(st.lsum + dpp_ror8(st.lsum)) * inv_vsc;
     // O of heads gA = 2*(kg&1), gB = gA + 1 in lanes kg = 0, 1: add pieces
     // (row pairs) and the page-1 rows held by lane group kg + 2
     const int gA = (2 * kg) & 3;
@@ -651,7 +672,8 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
         oB[t] = sum_halves(st.acc[t][2] + st.acc[t][3]);
     }
     const float LA = __shfl(L, gA * 2), LB = __shfl(L, gB * 2);
-    const float mA = __shfl(st.m, gA * 2), mB = __shfl(st.m, gB * 2);
+    const float m_true = st.m * c.sm;  // log2 domain
+    const float mA = __shfl(m_true, gA * 2), mB = __shfl(m_true, gB * 2);
 
     // the slot is idle now (every load has landed): it holds this wave's
     // result for the workgroup merge
@@ -821,6 +843,51 @@ int launch_d(gla_ctx *ctx, const Q8Params &prm, dim3 grid) {
     return GLA_OK;
 }
 
+// Workgroups of decode_q8_mfma_kernel<D> one CU holds at once (0 on error).
+template <int D>
+int resident_wgs() {
+    static int cached = -1;
+    if (cached < 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_q8_mfma_kernel<D>, kWaves * 64, 0) != hipSuccess)
+            n = 0;
+        cached = n;
+    }
+    return cached;
+}
+
+// Pages the window of one sequence spans, with seq_range's clamping.
+int host_seq_pages(int start, int len, int max_len, int pos_limit) {
+    start = start < 0 ? 0 : start;
+    len = len < 0 ? 0 : (len > max_len ? max_len : len);
+    int64_t e = (int64_t)start + len;
+    if (e > pos_limit) e = pos_limit;
+    const int64_t s = start > e ? e : start;
+    return e > s ? (int)(((e - 1) >> 4) - (s >> 4) + 1) : 0;
+}
+
+// Pages per chunk: 20 (10 steps), measured best on the Llama-3-8B and
+// Gemma-2-9B batch decodes (chunk sizes 12..52 span ~20%: shorter chunks
+// repeat the q / page-id / V-scale set-up more often, longer ones leave the
+// grid's last workgroups running alone). A batch too small to give every
+// resident workgroup slot a workgroup at 20 gets shorter chunks, down to 2.
+// With the pages of every sequence known (np) the counts are exact; without
+// them every sequence is taken to span max_pages.
+int choose_chunk_pages(const std::vector<int> &np, int n_seqs, int max_pages, int n_hu, int64_t slots) {
+    const int lo = std::max(2, (max_pages + kMaxChunks - 1) / kMaxChunks);
+    int ch = std::max(20, (lo + 1) & ~1);
+    for (; ch > 2 && ch - 2 >= lo; ch -= 2) {
+        int64_t wgs = 0;
+        if (np.empty()) {
+            wgs = (int64_t)n_seqs * (((max_pages + ch - 1) / ch + kWaves - 1) / kWaves);
+        } else {
+            for (int n : np) wgs += ((n + ch - 1) / ch + kWaves - 1) / kWaves;
+        }
+        if (wgs * n_hu >= slots) break;
+    }
+    return ch;
+}
+
 }  // namespace
 
 int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
@@ -830,18 +897,25 @@ int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
     // pages a window can span (a start inside a page adds one)
     const int64_t max_pages = d.max_kv_len > 0 ? (d.max_kv_len + GLA_PAGE_SIZE - 1) / GLA_PAGE_SIZE + 1 : 1;
     const int64_t units = (int64_t)d.n_seqs * d.n_kv_heads * n_hg;
-    // Chunk size: about 8k wave-chunks over the longest sequence (a chunk's
-    // set-up costs a few memory round trips, so longer chunks pay off until
-    // the tail of the grid gets ragged), preferring at most kMaxChunks chunks
-    // per unit; even and 2..64 pages (a wave holds one page id per lane).
-    int64_t ch = std::max<int64_t>(2, units * max_pages / 8192);
-    ch = std::max<int64_t>(ch, (max_pages + kMaxChunks - 1) / kMaxChunks);
+    // Chunk size (pages per wave; even, and at most 64: a wave holds one page
+    // id per lane). See choose_chunk_pages.
+    std::vector<int> np;
+    if (d.kv_len_host) {
+        np.resize(d.n_seqs);
+        for (int b = 0; b < d.n_seqs; b++)
+            np[b] = host_seq_pages(d.kv_start_host[b], d.kv_len_host[b], d.max_kv_len, d.pm.pos_limit);
+    }
+    int per_cu = D == 64 ? resident_wgs<64>() : (D == 128 ? resident_wgs<128>() : resident_wgs<256>());
+    const int64_t slots = (int64_t)std::max(ctx->n_cu, 1) * std::max(per_cu, 1);
+    int64_t ch = choose_chunk_pages(np, d.n_seqs, (int)max_pages, d.n_kv_heads * n_hg, slots);
     if (const char *env = getenv("GLA_Q8_CHUNK_PAGES")) {
         const int v = atoi(env);
-        if (v > 0) ch = v;
+        if (v > 0) ch = std::min(64, (v + 1) & ~1);
     }
-    ch = std::min<int64_t>(64, (ch + 1) & ~int64_t(1));
-    const int64_t max_chunks = (max_pages + ch - 1) / ch;
+    // workgroups per unit: exact with host lengths, else the max_kv_len bound
+    int64_t max_pages_seen = max_pages;
+    if (!np.empty()) max_pages_seen = std::max(1, *std::max_element(np.begin(), np.end()));
+    const int64_t max_chunks = (max_pages_seen + ch - 1) / ch;
     const int64_t max_wg = (max_chunks + kWaves - 1) / kWaves;
 
     Q8Params prm;

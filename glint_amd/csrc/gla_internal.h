@@ -168,6 +168,8 @@ struct DecodeLaunch {
     float softcap;
     const float *q;
     float *out;
+    const int32_t *kv_start_host = nullptr;  // optional host copies (both or neither)
+    const int32_t *kv_len_host = nullptr;
 };
 int launch_decode(gla_ctx *ctx, const DecodeLaunch &d);
 int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d);

@@ -177,6 +177,14 @@ typedef struct gla_decode_args {
     float softcap; /* attn_logit_softcapping; <= 0 means none */
     const float *q; /* device [B][n_heads][head_dim] */
     float *out;     /* device [B][n_heads][head_dim] */
+    /* Optional host copies of kv_start / kv_len: both NULL, or both int32[B]
+     * holding the values of the device arrays. Read during the call only, to
+     * size the launch to the batch's real lengths (the engine keeps every
+     * sequence's position on the host, src/transformer/forward.rs:1468-1507,
+     * so passing them is free); without them the launch is sized for
+     * max_kv_len. */
+    const int32_t *kv_start_host;
+    const int32_t *kv_len_host;
 } gla_decode_args;
 
 int gla_decode(gla_ctx *ctx, const gla_decode_args *args);

@@ -69,8 +69,10 @@ class Pool:
             self.stores = [orc.paged_q8(kq, vq, kv_dim, pb.table[b:b + 1]) for b in range(len(pb.ctx))]
 
 
-def run_decode(be, kv, q, kv_start, kv_len, n_heads, scale, softcap=None, layer=0, table=None, seq_slot=None):
-    """gla_decode through device buffers; q [B][H][d] host -> out [B][H][d] host."""
+def run_decode(be, kv, q, kv_start, kv_len, n_heads, scale, softcap=None, layer=0, table=None, seq_slot=None,
+               host_lengths=True):
+    """gla_decode through device buffers; q [B][H][d] host -> out [B][H][d] host. host_lengths:
+    also pass the host copies of kv_start / kv_len (they only size the launch)."""
     B = q.shape[0]
     dq = be.buffer(np.ascontiguousarray(q, np.float32))
     dout = be.empty(q.nbytes)
@@ -82,6 +84,9 @@ def run_decode(be, kv, q, kv_start, kv_len, n_heads, scale, softcap=None, layer=
         kw["page_table_stride"] = table.shape[1]
     if seq_slot is not None:
         kw["seq_slot"] = be.buffer(np.asarray(seq_slot, np.int32))
+    if host_lengths:
+        kw["kv_start_host"] = np.asarray(kv_start, np.int32)
+        kw["kv_len_host"] = np.asarray(kv_len, np.int32)
     be.decode(kv, dq, dout, ds, dl, B, int(np.max(kv_len)) if B else 0, n_heads, scale, softcap, layer=layer, **kw)
     be.sync()
     return dout.download(q.shape)

@@ -67,3 +67,15 @@ def test_window_start_matches_oracle(hip_lib):
             for layer in (0, 1, 2, 5):
                 for pos in (0, 1, 6, 7, 15, 16, 100, 4095, 4096, 9000):
                     assert hip_lib.gla_window_start(pos, w, alt, layer) == orc.window_start(pos, w, bool(alt), layer)
+
+
+def test_decode_args_layout_matches_header():
+    """The ctypes mirror of gla_decode_args has the header's field order, ending with the
+    optional host copies of kv_start / kv_len."""
+    import re
+    from pathlib import Path
+    from glint_amd import _lib
+    hdr = (Path(__file__).resolve().parents[1] / "include" / "glint_attn.h").read_text()
+    body = hdr[hdr.index("typedef struct gla_decode_args"):hdr.index("} gla_decode_args;")]
+    names = re.findall(r"\b(\w+);", re.sub(r"/\*.*?\*/", "", body, flags=re.S))
+    assert names == [f for f, _ in _lib.DecodeArgs._fields_]

@@ -82,14 +82,40 @@ def test_seq_slot_selects_cache(backend):
     assert_close(got, want, what="seq_slot")
 
 
-def test_empty_window_gives_zero(backend):
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+def test_empty_window_gives_zero(backend, dtype):
     H, Hkv, d = 4, 1, 64
-    c = Contig(backend, "f32", 2, 1, 64, Hkv, d, seed=9)
+    c = Contig(backend, dtype, 2, 1, 64, Hkv, d, seed=9)
     q = synth.normal(10, (2, H, d))
     got = run_decode(backend, c.cache, q, [0, 5], [0, 3], H, 0.125)
     assert not got[0].any()
     want = _oracle_decode(c.stores, q, [0, 5], [0, 3], H, Hkv, d, 0.125)
     assert_close(got, want)
+
+
+@pytest.mark.parametrize("host_lengths", [True, False])
+@pytest.mark.parametrize("chunk", [None, "2", "16", "64"])
+def test_q8_chunk_sizes(backend, monkeypatch, chunk, host_lengths):
+    """Q8_0 decode with the default chunk size (sized from the host copies of the lengths, or
+    from max_kv_len without them) and forced ones (GLA_Q8_CHUNK_PAGES): 2-page chunks (many
+    partials per unit), 64-page chunks (the largest a wave holds). More than 64 sequences,
+    empty windows, single-page and single-position sequences, windows starting mid-page."""
+    if chunk is None:
+        monkeypatch.delenv("GLA_Q8_CHUNK_PAGES", raising=False)
+    else:
+        monkeypatch.setenv("GLA_Q8_CHUNK_PAGES", chunk)
+    H, Hkv, d = 8, 4, 64
+    ctx = synth.uniform_int(811, 1, 1500, 150)
+    ctx[[0, 7, 64, 65, 149]] = [0, 1, 16, 0, 2049]
+    pb = synth.paged_batch(812, ctx, prefix_tokens=48)
+    p = Pool(backend, "q8", pb, Hkv, d, seed=813)
+    q = synth.normal(814, (len(ctx), H, d))
+    w = synth.windowed(pb, 700)
+    want = _oracle_decode(p.stores, q, w.kv_start, w.kv_len, H, Hkv, d, 0.125)
+    got = run_decode(backend, p.pool, q, w.kv_start, w.kv_len, H, 0.125, table=pb.table,
+                     host_lengths=host_lengths)
+    assert not got[0].any() and not got[65].any()
+    assert_close(got, want, what=f"q8 chunk {chunk}")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "q8"])
