@@ -519,13 +519,11 @@ __device__ __forceinline__ void step_pv(RawV<D> &cur, const StepConst<D> &c, Ste
 // the wave's LDS slot ([kGT][D + 2] floats).
 template <int D>
 __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, int b, int kvh, int h_base,
-                                           int gcount, int chunk, int lane, uint8_t *slot) {
+                                           int gcount, int pg0, int npg, int lane, uint8_t *slot) {
     constexpr int NB = D / 32;  // Q8_0 blocks per head row
     constexpr int ND = D / 16;  // 16-wide d tiles of O
     const int kg = lane >> 4;   // lane group: MFMA k-slots kg*8 .. kg*8+7
     const int lc = lane & 15;   // S column / P' row / O column of the lane
-    const int pg0 = r.fp + chunk * p.ch;
-    const int npg = min(p.ch, r.fp + r.n_pages - pg0);
     const int nsteps = (npg + 1) >> 1;
 
     // q and the chunk's page ids are loaded together (the streaming loads
@@ -724,13 +722,20 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
             for (int idx = tid; idx < gcount * D; idx += kThreads) out[idx] = 0.0f;
         return;
     }
-    const int n_chunks = (r.n_pages + p.ch - 1) / p.ch;
-    const int n_wg = (n_chunks + kWaves - 1) / kWaves;
+    // A workgroup covers kWaves * ch pages of the unit (the last one what is
+    // left) and splits them evenly over its waves, so the waves of the
+    // sequence's last, short workgroup finish together instead of one wave
+    // working while the others wait at the merge.
+    const int span = kWaves * p.ch;
+    const int n_wg = (r.n_pages + span - 1) / span;
     const int wg = blockIdx.y;
     if (wg >= n_wg) return;
-    const int chunk = wg * kWaves + wave;
-    if (chunk < n_chunks) {
-        wave_chunk<D>(p, r, b, kvh, h_base, gcount, chunk, lane, slots[wave]);
+    const int wg_pages = min(span, r.n_pages - wg * span);
+    const int per_wave = ((wg_pages + 2 * kWaves - 1) / (2 * kWaves)) * 2;  // even: a step is two pages
+    const int my0 = wave * per_wave;
+    if (my0 < wg_pages) {
+        wave_chunk<D>(p, r, b, kvh, h_base, gcount, r.fp + wg * span + my0, min(per_wave, wg_pages - my0), lane,
+                      slots[wave]);
     } else if (lane < kGT) {
         float *res = reinterpret_cast<float *>(slots[wave]);
         res[lane * (D + 2) + D] = -INFINITY;
@@ -788,8 +793,8 @@ __global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p
     const int gcount = min(kGT, p.group - g0);
     const int h_base = kvh * p.group + g0;
     const Range r = seq_range(p, b);
-    const int n_chunks = (r.n_pages + p.ch - 1) / p.ch;
-    const int n_wg = (n_chunks + kWaves - 1) / kWaves;
+    const int span = kWaves * p.ch;  // pages per workgroup
+    const int n_wg = (r.n_pages + span - 1) / span;
     if (n_wg <= 1) return;
     const int idx = blockIdx.x * 256 + threadIdx.x;
     const int g = idx / D;
