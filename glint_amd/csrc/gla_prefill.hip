@@ -61,22 +61,31 @@ __device__ __forceinline__ int window_lo(int pos, int w) {
     return s > 0 ? s : 0;
 }
 
-// Stage K (row stride D+2 floats) and V (row stride D+4 floats) of keys
-// [k0, k0+KT) in LDS as f32; keys outside [klo, khi] are zero.
+// One tile's K/V as f32 in registers: thread u of the workgroup holds 16
+// consecutive elements (unit u / (D/16) is the key, unit % (D/16) the
+// 16-element column block) of K and of V; keys outside [klo, khi] are zero.
+template <int D>
+struct TileRegs {
+    static constexpr int UNITS = KT * D / 16;
+    static constexpr int PER_THREAD = (UNITS + kThreads - 1) / kThreads;
+    float4 k[PER_THREAD][4];
+    float4 v[PER_THREAD][4];
+};
+
 template <int D, bool Q8>
-__device__ __forceinline__ void load_tile(const PrefillParams &p, int b, int kvh, int k0, int klo, int khi,
-                                          float *Ks, float *Vs) {
-    constexpr int UNITS = KT * D / 16;  // 16 elements per unit
+__device__ __forceinline__ void fetch_tile(const PrefillParams &p, int b, int kvh, int k0, int klo, int khi,
+                                           TileRegs<D> &t) {
     const int64_t head_off = (int64_t)kvh * p.kv.head_stride;
-    for (int u = threadIdx.x; u < UNITS; u += kThreads) {
+#pragma unroll
+    for (int j = 0; j < TileRegs<D>::PER_THREAD; j++) {
+        const int u = threadIdx.x + j * kThreads;
         const int key = u / (D / 16);
         const int c16 = u - key * (D / 16);
         const int kp = k0 + key;
         float kf[16], vf[16];
-        if (kp >= klo && kp <= khi) {
+        if (u < TileRegs<D>::UNITS && kp >= klo && kp <= khi) {
             const int64_t pid = map_page(p.pm, b, kp >> 4);
             const int slot = kp & 15;
-            const int64_t base = pid * p.kv.page_stride + head_off + (int64_t)slot * p.kv.row_stride;
             if constexpr (Q8) {
                 // quants in the decode kernel's MFMA operand order (gla_internal.h)
                 const int64_t hb = pid * p.kv.page_stride + head_off;
@@ -87,59 +96,84 @@ __device__ __forceinline__ void load_tile(const PrefillParams &p, int b, int kvh
 #pragma unroll
                 for (int e = 0; e < 16; e++)
                     vw4[e >> 2] |= (uint32_t)p.kv.v[hb + q8v_off(slot, c16 * 16 + e, D)] << ((e & 3) * 8);
-                const uint4 vq = make_uint4(vw4[0], vw4[1], vw4[2], vw4[3]);
                 const int blk = (c16 * 16) >> 5;
                 const uint16_t *ksp = reinterpret_cast<const uint16_t *>(p.kv.ks + hb) + q8ks_off(slot, blk, D);
                 const uint16_t *vsp = reinterpret_cast<const uint16_t *>(p.kv.vs + hb) + slot * (D / 32) + blk;
                 const float ksc = __half2float(__ushort_as_half(*ksp));
                 const float vsc = __half2float(__ushort_as_half(*vsp));
                 const uint32_t kw[4] = {kq.x, kq.y, kq.z, kq.w};
-                const uint32_t vw[4] = {vq.x, vq.y, vq.z, vq.w};
 #pragma unroll
                 for (int e = 0; e < 16; e++) {  // stored quants are x + 128
                     kf[e] = (float)((int)((kw[e >> 2] >> ((e & 3) * 8)) & 0xff) - 128) * ksc;
-                    vf[e] = (float)((int)((vw[e >> 2] >> ((e & 3) * 8)) & 0xff) - 128) * vsc;
+                    vf[e] = (float)((int)((vw4[e >> 2] >> ((e & 3) * 8)) & 0xff) - 128) * vsc;
                 }
             } else {
+                const int64_t base = pid * p.kv.page_stride + head_off + (int64_t)slot * p.kv.row_stride;
                 const float4 *kp4 = reinterpret_cast<const float4 *>(p.kv.k + base) + c16 * 4;
                 const float4 *vp4 = reinterpret_cast<const float4 *>(p.kv.v + base) + c16 * 4;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float4 a = kp4[j];
-                    const float4 c = vp4[j];
-                    kf[4 * j] = a.x;
-                    kf[4 * j + 1] = a.y;
-                    kf[4 * j + 2] = a.z;
-                    kf[4 * j + 3] = a.w;
-                    vf[4 * j] = c.x;
-                    vf[4 * j + 1] = c.y;
-                    vf[4 * j + 2] = c.z;
-                    vf[4 * j + 3] = c.w;
+                for (int q = 0; q < 4; q++) {
+                    t.k[j][q] = kp4[q];
+                    t.v[j][q] = vp4[q];
                 }
+                continue;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                t.k[j][q] = make_float4(kf[4 * q], kf[4 * q + 1], kf[4 * q + 2], kf[4 * q + 3]);
+                t.v[j][q] = make_float4(vf[4 * q], vf[4 * q + 1], vf[4 * q + 2], vf[4 * q + 3]);
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                kf[e] = 0.0f;
-                vf[e] = 0.0f;
+            for (int q = 0; q < 4; q++) {
+                t.k[j][q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                t.v[j][q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
         }
-        float2 *kd = reinterpret_cast<float2 *>(Ks + key * (D + 2) + c16 * 16);
-#pragma unroll
-        for (int j = 0; j < 8; j++) kd[j] = make_float2(kf[2 * j], kf[2 * j + 1]);
-        float4 *vd = reinterpret_cast<float4 *>(Vs + key * (D + 4) + c16 * 16);
-#pragma unroll
-        for (int j = 0; j < 4; j++) vd[j] = make_float4(vf[4 * j], vf[4 * j + 1], vf[4 * j + 2], vf[4 * j + 3]);
     }
 }
 
+// K and V rows in LDS: D floats + 4 of padding, so the 16 rows a 16-lane
+// group reads with 16-byte loads start in distinct bank groups.
+template <int D>
+constexpr int kRow = D + 4;
+
+template <int D>
+__device__ __forceinline__ void store_tile(const TileRegs<D> &t, float *Ks, float *Vs) {
+#pragma unroll
+    for (int j = 0; j < TileRegs<D>::PER_THREAD; j++) {
+        const int u = threadIdx.x + j * kThreads;
+        if (u >= TileRegs<D>::UNITS) break;
+        const int key = u / (D / 16);
+        const int c16 = u - key * (D / 16);
+        float4 *kd = reinterpret_cast<float4 *>(Ks + key * kRow<D> + c16 * 16);
+        float4 *vd = reinterpret_cast<float4 *>(Vs + key * kRow<D> + c16 * 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            kd[q] = t.k[j][q];
+            vd[q] = t.v[j][q];
+        }
+    }
+}
+
+// Workgroup: 4 waves; a wave owns 16*NT queries of one q-head, the HPW
+// heads of the workgroup share one KV head. K/V tiles of KT keys are
+// double-buffered in LDS: the next tile is fetched into registers while the
+// current one is multiplied, then stored to the other buffer, with one
+// barrier per tile.
+// Reduction order. Lane group g (lanes 16g..16g+15) covers the head
+// dimensions [g*D/4, (g+1)*D/4): k-step s of S^T = K.Q^T multiplies d =
+// g*D/4 + s, so a lane reads its K operands four at a time from one row.
+// O^T row R of d-tile t is d = R*DT + t, so the V^T operands a lane needs
+// for one key are DT consecutive floats, and a lane's outputs for a query
+// are the 4*DT consecutive floats [4g*DT, 4(g+1)*DT).
 template <int D, int NT, bool Q8>
 __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillParams p) {
     constexpr int QW = 16 * NT;  // queries per wave
     constexpr int KS = D / 4;    // k-steps of S = K Q^T
     constexpr int DT = D / 16;   // d tiles of O
-    __shared__ float Ks[KT * (D + 2)];
-    __shared__ float Vs[KT * (D + 4)];
+    __shared__ __attribute__((aligned(16))) float Ks[2][KT * kRow<D>];
+    __shared__ __attribute__((aligned(16))) float Vs[2][KT * kRow<D>];
 
     const int b = blockIdx.z;
     const int n_hgrp = p.group / p.hpw;
@@ -168,15 +202,22 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
     const int khi = min(pos0 + q_last, p.pm.pos_limit - 1);
     const int klo = window_lo(pos0 + qb0, p.sliding_window);
 
-    // Q^T fragments: qf[nt][s] = Q[query nt*16 + lrow][d = 4s + lgrp]
+    // Q^T fragments: qf[nt][s] = Q[query nt*16 + lrow][d = lgrp*KS + s]
     float qf[NT][KS];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int lq = wq0 + nt * 16 + lrow;
         const bool ok = lq < q_len;
-        const float *qp = p.q + ((int64_t)(row0 + (ok ? lq : 0)) * p.n_heads + head) * D;
+        const float4 *qp = reinterpret_cast<const float4 *>(
+            p.q + ((int64_t)(row0 + (ok ? lq : 0)) * p.n_heads + head) * D + lgrp * KS);
 #pragma unroll
-        for (int s = 0; s < KS; s++) qf[nt][s] = ok ? qp[4 * s + lgrp] * p.q_mul : 0.0f;
+        for (int s4 = 0; s4 < KS / 4; s4++) {
+            const float4 v = qp[s4];
+            qf[nt][4 * s4 + 0] = ok ? v.x * p.q_mul : 0.0f;
+            qf[nt][4 * s4 + 1] = ok ? v.y * p.q_mul : 0.0f;
+            qf[nt][4 * s4 + 2] = ok ? v.z * p.q_mul : 0.0f;
+            qf[nt][4 * s4 + 3] = ok ? v.w * p.q_mul : 0.0f;
+        }
     }
 
     floatx4 o[DT][NT];
@@ -196,10 +237,17 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
     }
 
     if (khi >= klo) {
-        for (int k0 = (klo / KT) * KT; k0 <= khi; k0 += KT) {
-            __syncthreads();
-            load_tile<D, Q8>(p, b, kvh, k0, klo, khi, Ks, Vs);
-            __syncthreads();
+        const int kfirst = (klo / KT) * KT;
+        TileRegs<D> tr;
+        fetch_tile<D, Q8>(p, b, kvh, kfirst, klo, khi, tr);
+        store_tile<D>(tr, Ks[0], Vs[0]);
+        __syncthreads();
+        int buf = 0;
+        for (int k0 = kfirst; k0 <= khi; k0 += KT, buf ^= 1) {
+            const bool more = k0 + KT <= khi;
+            if (more) fetch_tile<D, Q8>(p, b, kvh, k0 + KT, klo, khi, tr);
+            const float *ks = Ks[buf];
+            const float *vs = Vs[buf];
 
             // S^T = K . Q^T
             floatx4 sacc[2][NT];
@@ -208,13 +256,18 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) sacc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int s = 0; s < KS; s++) {
+            for (int s4 = 0; s4 < KS / 4; s4++) {
 #pragma unroll
                 for (int mt = 0; mt < 2; mt++) {
-                    const float a = Ks[(mt * 16 + lrow) * (D + 2) + 4 * s + lgrp];
+                    const float4 a = *reinterpret_cast<const float4 *>(ks + (mt * 16 + lrow) * kRow<D> + lgrp * KS +
+                                                                       4 * s4);
+                    const float av[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-                    for (int nt = 0; nt < NT; nt++)
-                        sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qf[nt][s], sacc[mt][nt], 0, 0, 0);
+                    for (int e = 0; e < 4; e++)
+#pragma unroll
+                        for (int nt = 0; nt < NT; nt++)
+                            sacc[mt][nt] =
+                                __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], qf[nt][4 * s4 + e], sacc[mt][nt], 0, 0, 0);
                 }
             }
 
@@ -266,20 +319,30 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
             for (int mt = 0; mt < 2; mt++) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float *vrow = Vs + (mt * 16 + 4 * lgrp + i) * (D + 4) + lrow;
+                    const float *vrow = vs + (mt * 16 + 4 * lgrp + i) * kRow<D> + lrow * DT;
+                    float av[DT];
 #pragma unroll
-                    for (int t = 0; t < DT; t++) {
-                        const float a = vrow[16 * t];
+                    for (int t4 = 0; t4 < DT / 4; t4++) {
+                        const float4 a = reinterpret_cast<const float4 *>(vrow)[t4];
+                        av[4 * t4] = a.x;
+                        av[4 * t4 + 1] = a.y;
+                        av[4 * t4 + 2] = a.z;
+                        av[4 * t4 + 3] = a.w;
+                    }
+#pragma unroll
+                    for (int t = 0; t < DT; t++)
 #pragma unroll
                         for (int nt = 0; nt < NT; nt++)
-                            o[t][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, sacc[mt][nt][i], o[t][nt], 0, 0, 0);
-                    }
+                            o[t][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t], sacc[mt][nt][i], o[t][nt], 0, 0, 0);
                 }
             }
+
+            if (more) store_tile<D>(tr, Ks[buf ^ 1], Vs[buf ^ 1]);
+            __syncthreads();
         }
     }
 
-    // normalise and store: lane holds O^T[16t + 4*lgrp + r][query lrow]
+    // normalise and store: lane holds O^T[d = (4*lgrp + r)*DT + t][query lrow]
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         float lt = lpart[nt];
@@ -288,12 +351,14 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
         const int lq = wq0 + nt * 16 + lrow;
         if (lq >= q_len) continue;
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-        float *op = p.out + ((int64_t)(row0 + lq) * p.n_heads + head) * D;
+        float *op = p.out + ((int64_t)(row0 + lq) * p.n_heads + head) * D + 4 * lgrp * DT;
 #pragma unroll
-        for (int t = 0; t < DT; t++) {
-            const floatx4 v = o[t][nt] * inv;
-            *reinterpret_cast<float4 *>(op + 16 * t + 4 * lgrp) = make_float4(v[0], v[1], v[2], v[3]);
-        }
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int t4 = 0; t4 < DT / 4; t4++)
+                *reinterpret_cast<float4 *>(op + r * DT + 4 * t4) =
+                    make_float4(o[4 * t4][nt][r] * inv, o[4 * t4 + 1][nt][r] * inv, o[4 * t4 + 2][nt][r] * inv,
+                                o[4 * t4 + 3][nt][r] * inv);
     }
 }
 
