@@ -23,7 +23,6 @@ namespace gla {
 
 namespace {
 
-constexpr int kThreads = 256;
 constexpr int KT = 32;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -64,26 +63,26 @@ __device__ __forceinline__ int window_lo(int pos, int w) {
 // One tile's K/V as f32 in registers: thread u of the workgroup holds 16
 // consecutive elements (unit u / (D/16) is the key, unit % (D/16) the
 // 16-element column block) of K and of V; keys outside [klo, khi] are zero.
-template <int D>
+template <int D, int NTHR>
 struct TileRegs {
     static constexpr int UNITS = KT * D / 16;
-    static constexpr int PER_THREAD = (UNITS + kThreads - 1) / kThreads;
+    static constexpr int PER_THREAD = (UNITS + NTHR - 1) / NTHR;
     float4 k[PER_THREAD][4];
     float4 v[PER_THREAD][4];
 };
 
-template <int D, bool Q8>
+template <int D, int NTHR, bool Q8>
 __device__ __forceinline__ void fetch_tile(const PrefillParams &p, int b, int kvh, int k0, int klo, int khi,
-                                           TileRegs<D> &t) {
+                                           TileRegs<D, NTHR> &t) {
     const int64_t head_off = (int64_t)kvh * p.kv.head_stride;
 #pragma unroll
-    for (int j = 0; j < TileRegs<D>::PER_THREAD; j++) {
-        const int u = threadIdx.x + j * kThreads;
+    for (int j = 0; j < TileRegs<D, NTHR>::PER_THREAD; j++) {
+        const int u = threadIdx.x + j * NTHR;
         const int key = u / (D / 16);
         const int c16 = u - key * (D / 16);
         const int kp = k0 + key;
         float kf[16], vf[16];
-        if (u < TileRegs<D>::UNITS && kp >= klo && kp <= khi) {
+        if (u < TileRegs<D, NTHR>::UNITS && kp >= klo && kp <= khi) {
             const int64_t pid = map_page(p.pm, b, kp >> 4);
             const int slot = kp & 15;
             if constexpr (Q8) {
@@ -138,12 +137,12 @@ __device__ __forceinline__ void fetch_tile(const PrefillParams &p, int b, int kv
 template <int D>
 constexpr int kRow = D + 4;
 
-template <int D>
-__device__ __forceinline__ void store_tile(const TileRegs<D> &t, float *Ks, float *Vs) {
+template <int D, int NTHR>
+__device__ __forceinline__ void store_tile(const TileRegs<D, NTHR> &t, float *Ks, float *Vs) {
 #pragma unroll
-    for (int j = 0; j < TileRegs<D>::PER_THREAD; j++) {
-        const int u = threadIdx.x + j * kThreads;
-        if (u >= TileRegs<D>::UNITS) break;
+    for (int j = 0; j < TileRegs<D, NTHR>::PER_THREAD; j++) {
+        const int u = threadIdx.x + j * NTHR;
+        if (u >= TileRegs<D, NTHR>::UNITS) break;
         const int key = u / (D / 16);
         const int c16 = u - key * (D / 16);
         float4 *kd = reinterpret_cast<float4 *>(Ks + key * kRow<D> + c16 * 16);
@@ -156,8 +155,8 @@ __device__ __forceinline__ void store_tile(const TileRegs<D> &t, float *Ks, floa
     }
 }
 
-// Workgroup: 4 waves; a wave owns 16*NT queries of one q-head, the HPW
-// heads of the workgroup share one KV head. K/V tiles of KT keys are
+// Workgroup: NW waves; a wave owns 16*NT queries of one q-head, the HPW
+// heads of the workgroup share one KV head (NW / HPW waves per head). K/V tiles of KT keys are
 // double-buffered in LDS: the next tile is fetched into registers while the
 // current one is multiplied, then stored to the other buffer, with one
 // barrier per tile.
@@ -167,8 +166,9 @@ __device__ __forceinline__ void store_tile(const TileRegs<D> &t, float *Ks, floa
 // O^T row R of d-tile t is d = R*DT + t, so the V^T operands a lane needs
 // for one key are DT consecutive floats, and a lane's outputs for a query
 // are the 4*DT consecutive floats [4g*DT, 4(g+1)*DT).
-template <int D, int NT, bool Q8>
-__global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillParams p) {
+template <int D, int NT, int NW, bool Q8>
+__global__ __launch_bounds__(NW * 64) void prefill_f32_kernel(const PrefillParams p) {
+    constexpr int NTHR = NW * 64;
     constexpr int QW = 16 * NT;  // queries per wave
     constexpr int KS = D / 4;    // k-steps of S = K Q^T
     constexpr int DT = D / 16;   // d tiles of O
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
     const int kvh = blockIdx.y / n_hgrp;
     const int hgrp = blockIdx.y - kvh * n_hgrp;
     const int qblk = p.n_qblocks - 1 - (int)blockIdx.x;  // longest rows first
-    const int waves_per_head = 4 / p.hpw;
+    const int waves_per_head = NW / p.hpw;
     const int qwg = QW * waves_per_head;
 
     const int row0 = p.q_start[b];
@@ -238,14 +238,14 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
 
     if (khi >= klo) {
         const int kfirst = (klo / KT) * KT;
-        TileRegs<D> tr;
-        fetch_tile<D, Q8>(p, b, kvh, kfirst, klo, khi, tr);
-        store_tile<D>(tr, Ks[0], Vs[0]);
+        TileRegs<D, NTHR> tr;
+        fetch_tile<D, NTHR, Q8>(p, b, kvh, kfirst, klo, khi, tr);
+        store_tile<D, NTHR>(tr, Ks[0], Vs[0]);
         __syncthreads();
         int buf = 0;
         for (int k0 = kfirst; k0 <= khi; k0 += KT, buf ^= 1) {
             const bool more = k0 + KT <= khi;
-            if (more) fetch_tile<D, Q8>(p, b, kvh, k0 + KT, klo, khi, tr);
+            if (more) fetch_tile<D, NTHR, Q8>(p, b, kvh, k0 + KT, klo, khi, tr);
             const float *ks = Ks[buf];
             const float *vs = Vs[buf];
 
@@ -257,21 +257,31 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
                 for (int nt = 0; nt < NT; nt++) sacc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s4 = 0; s4 < KS / 4; s4++) {
+                float av[2][4];
 #pragma unroll
                 for (int mt = 0; mt < 2; mt++) {
                     const float4 a = *reinterpret_cast<const float4 *>(ks + (mt * 16 + lrow) * kRow<D> + lgrp * KS +
                                                                        4 * s4);
-                    const float av[4] = {a.x, a.y, a.z, a.w};
+                    av[mt][0] = a.x;
+                    av[mt][1] = a.y;
+                    av[mt][2] = a.z;
+                    av[mt][3] = a.w;
+                }
+                // the 2*NT accumulators in turn: a dependent MFMA every 2*NT issues
 #pragma unroll
-                    for (int e = 0; e < 4; e++)
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int mt = 0; mt < 2; mt++)
 #pragma unroll
                         for (int nt = 0; nt < NT; nt++)
                             sacc[mt][nt] =
-                                __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], qf[nt][4 * s4 + e], sacc[mt][nt], 0, 0, 0);
-                }
+                                __builtin_amdgcn_mfma_f32_16x16x4f32(av[mt][e], qf[nt][4 * s4 + e], sacc[mt][nt], 0, 0, 0);
             }
 
-            // online softmax over this tile, per query column
+            // online softmax over this tile, per query column. Only tiles that
+            // cross the diagonal, a window edge or the key range need the mask.
+            const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
+                                  (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 float mx = -INFINITY;
@@ -282,8 +292,10 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
                         const int kp = k0 + mt * 16 + 4 * lgrp + i;
                         float x = sacc[mt][nt][i];
                         if (p.softcap > 0.0f) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
-                        const bool ok = kp <= qpos[nt] && kp >= qlo[nt] && kp >= klo && kp <= khi;
-                        x = ok ? x : -INFINITY;
+                        if (!interior) {
+                            const bool ok = kp <= qpos[nt] && kp >= qlo[nt] && kp >= klo && kp <= khi;
+                            x = ok ? x : -INFINITY;
+                        }
                         sacc[mt][nt][i] = x;
                         mx = fmaxf(mx, x);
                     }
@@ -310,8 +322,10 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
                         ls += pv;
                     }
                 lpart[nt] = lpart[nt] * rs + ls;
+                if (__ballot(rs != 1.0f)) {  // the running max moved for some query
 #pragma unroll
-                for (int t = 0; t < DT; t++) o[t][nt] *= rs;
+                    for (int t = 0; t < DT; t++) o[t][nt] *= rs;
+                }
             }
 
             // O^T += V^T . P^T
@@ -337,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
                 }
             }
 
-            if (more) store_tile<D>(tr, Ks[buf ^ 1], Vs[buf ^ 1]);
+            if (more) store_tile<D, NTHR>(tr, Ks[buf ^ 1], Vs[buf ^ 1]);
             __syncthreads();
         }
     }
@@ -362,12 +376,37 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillPara
     }
 }
 
-template <int D, int NT, bool Q8>
+template <int D, int NT, int NW, bool Q8>
 int launch_f32(gla_ctx *ctx, const PrefillParams &prm, dim3 grid) {
-    hipLaunchKernelGGL((prefill_f32_kernel<D, NT, Q8>), grid, dim3(kThreads), 0, ctx->stream, prm);
+    hipLaunchKernelGGL((prefill_f32_kernel<D, NT, NW, Q8>), grid, dim3(NW * 64), 0, ctx->stream, prm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "prefill_f32_kernel launch: %s", hipGetErrorString(e));
     return GLA_OK;
+}
+
+// Shapes per head_dim: queries per wave (16*NT) and waves per workgroup.
+// d128 (cfg4): 4 waves of 32 queries. 8 waves of 16 queries (4 waves per
+// SIMD instead of 2) measured 4% slower: each K/V operand read from LDS then
+// feeds one MFMA instead of two.
+template <int D>
+struct PrefillShape;
+template <>
+struct PrefillShape<64> {
+    static constexpr int NT = 2, NW = 4;
+};
+template <>
+struct PrefillShape<128> {
+    static constexpr int NT = 2, NW = 4;
+};
+template <>
+struct PrefillShape<256> {
+    static constexpr int NT = 1, NW = 4;
+};
+
+template <int D>
+int launch_shape(gla_ctx *ctx, bool q8, const PrefillParams &prm, dim3 grid) {
+    using S = PrefillShape<D>;
+    return q8 ? launch_f32<D, S::NT, S::NW, true>(ctx, prm, grid) : launch_f32<D, S::NT, S::NW, false>(ctx, prm, grid);
 }
 
 }  // namespace
@@ -376,8 +415,21 @@ int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
     const int D = a.head_dim;
     const int group = a.n_heads / a.n_kv_heads;
     const int hpw = (group % 4 == 0) ? 4 : ((group % 2 == 0) ? 2 : 1);
-    const int NT = D <= 128 ? 2 : 1;
-    const int qwg = 16 * NT * (4 / hpw);
+    int NT = 1, NW = 4;
+    switch (D) {
+    case 64:
+        NT = PrefillShape<64>::NT, NW = PrefillShape<64>::NW;
+        break;
+    case 128:
+        NT = PrefillShape<128>::NT, NW = PrefillShape<128>::NW;
+        break;
+    case 256:
+        NT = PrefillShape<256>::NT, NW = PrefillShape<256>::NW;
+        break;
+    default:
+        return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
+    }
+    const int qwg = 16 * NT * (NW / hpw);
     PrefillParams prm;
     prm.kv = a.kv;
     prm.pm = a.pm;
@@ -401,13 +453,12 @@ int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
     dim3 grid(prm.n_qblocks, a.n_kv_heads * (group / hpw), a.n_seqs);
     switch (D) {
     case 64:
-        return a.q8 ? launch_f32<64, 2, true>(ctx, prm, grid) : launch_f32<64, 2, false>(ctx, prm, grid);
+        return launch_shape<64>(ctx, a.q8, prm, grid);
     case 128:
-        return a.q8 ? launch_f32<128, 2, true>(ctx, prm, grid) : launch_f32<128, 2, false>(ctx, prm, grid);
-    case 256:
-        return a.q8 ? launch_f32<256, 1, true>(ctx, prm, grid) : launch_f32<256, 1, false>(ctx, prm, grid);
+        return launch_shape<128>(ctx, a.q8, prm, grid);
+    default:
+        return launch_shape<256>(ctx, a.q8, prm, grid);
     }
-    return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
 }
 
 }  // namespace gla
