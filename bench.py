@@ -455,6 +455,16 @@ def main() -> int:
         if not args.no_cpu:
             secondary["cfg4_f32"]["cpu_baseline"] = wl.cpu_baseline()
         log(f"cfg4 f32: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
+        # bf16-input variant: same inputs rounded to bf16 inside the kernel
+        wl.precision = "bf16"
+        ms = time_steps(be, ev, wl.step, max(3, args.steps // 5), min(args.warmup, 2))
+        tf = wl.flops_per_step() / (ms * 1e-3) / 1e12
+        secondary["cfg4_bf16"] = {
+            "workload": "Llama-3-8B causal prefill 4x2048, f32 KV cache, bf16-input MFMA (fp32 accumulate)",
+            "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+            "frac_of_bf16_mfma_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
+            "tolerance": "max abs 3e-2 / rel 3e-2 vs the fp32 oracle (tests/test_gpu_prefill.py)"}
+        log(f"cfg4 bf16: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
         del wl
     if args.calibrate:
         log("calibration copies")

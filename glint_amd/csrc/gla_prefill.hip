@@ -376,6 +376,326 @@ __global__ __launch_bounds__(NW * 64) void prefill_f32_kernel(const PrefillParam
     }
 }
 
+// ---------------------------------------------------------------------------
+// bf16-input variant: Q, K, V and the probabilities are rounded to bf16 and
+// both products run on v_mfma_f32_16x16x32_bf16 with fp32 accumulation; the
+// softmax stays fp32. Same workgroup shape, masks and online softmax as the
+// fp32 kernel. K is staged row-major and V transposed (Vt[d][key]) in LDS
+// as bf16, so every MFMA operand a lane needs is one 8- or 16-byte read.
+//   S^T[key][q] = K . Q^T   A = K (16 keys x 32 d), B = Q^T from registers
+//   O^T[d][q]  += V^T . P^T A = Vt (16 d x 32 keys), B = P^T packed from the
+//                           S^T accumulators: k-slots 0..3 of lane group g
+//                           are keys 4g+r of the first 16-key half and 4..7
+//                           the same keys of the second half, which is what
+//                           the lane's two accumulators hold.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+template <int D>
+constexpr int kKRowH = D + 8;  // K row in LDS (bf16): 16 bytes of padding
+constexpr int kVtRowH = KT + 8;  // Vt row in LDS (bf16): 32 keys + 16 bytes
+
+// The 4 keys x 4 dims block of K and of V that one thread stages, as f32.
+struct Block44 {
+    float4 k[4];  // k[i] = K[key 4*kq + i][4*dq .. 4*dq+3]
+    float4 v[4];  // v[i] = V[key 4*kq + i][4*dq .. 4*dq+3]
+};
+
+template <int D, bool Q8>
+__device__ __forceinline__ void fetch_block44(const PrefillParams &p, int b, int kvh, int key0, int d0, int klo,
+                                              int khi, Block44 &o) {
+    const int64_t head_off = (int64_t)kvh * p.kv.head_stride;
+    // key0 is a multiple of 4, so the 4 keys share one page
+    const int64_t pid = map_page(p.pm, b, key0 >> 4);
+    if constexpr (Q8) {
+        const int64_t hb = pid * p.kv.page_stride + head_off;
+        const int slot0 = key0 & 15;
+        const int blk = d0 >> 5;
+        const uint16_t *vsp = reinterpret_cast<const uint16_t *>(p.kv.vs + hb);
+        const uint16_t *ksp = reinterpret_cast<const uint16_t *>(p.kv.ks + hb);
+        // V: 4 consecutive slots of one d are 4 consecutive bytes (q8v_off)
+        float vq[4][4];  // [d][key]
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t w = *reinterpret_cast<const uint32_t *>(p.kv.v + hb + q8v_off(slot0, d0 + j, D));
+#pragma unroll
+            for (int i = 0; i < 4; i++) vq[j][i] = (float)((int)((w >> (8 * i)) & 0xff) - 128);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int kp = key0 + i;
+            const bool ok = kp >= klo && kp <= khi;
+            // K: 4 consecutive d of one slot are 4 consecutive bytes (q8k_off)
+            const uint32_t w = *reinterpret_cast<const uint32_t *>(p.kv.k + hb + q8k_off(slot0 + i, d0, D));
+            const float ksc = ok ? __half2float(__ushort_as_half(ksp[q8ks_off(slot0 + i, blk, D)])) : 0.0f;
+            const float vsc = ok ? __half2float(__ushort_as_half(vsp[(slot0 + i) * (D / 32) + blk])) : 0.0f;
+            o.k[i] = make_float4((float)((int)(w & 0xff) - 128) * ksc, (float)((int)((w >> 8) & 0xff) - 128) * ksc,
+                                 (float)((int)((w >> 16) & 0xff) - 128) * ksc,
+                                 (float)((int)((w >> 24) & 0xff) - 128) * ksc);
+            o.v[i] = make_float4(vq[0][i] * vsc, vq[1][i] * vsc, vq[2][i] * vsc, vq[3][i] * vsc);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int kp = key0 + i;
+            if (kp >= klo && kp <= khi) {
+                const int64_t base =
+                    pid * p.kv.page_stride + head_off + (int64_t)((kp & 15)) * p.kv.row_stride + (int64_t)d0 * 4;
+                o.k[i] = *reinterpret_cast<const float4 *>(p.kv.k + base);
+                o.v[i] = *reinterpret_cast<const float4 *>(p.kv.v + base);
+            } else {
+                o.k[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                o.v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ bf16x4 to_bf16x4(float a, float b, float c, float d) {
+    return bf16x4{(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
+}
+
+template <int D>
+__device__ __forceinline__ void store_block44(const Block44 &o, int kq, int dq, __bf16 *Kh, __bf16 *Vt) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        *reinterpret_cast<bf16x4 *>(Kh + (4 * kq + i) * kKRowH<D> + 4 * dq) =
+            to_bf16x4(o.k[i].x, o.k[i].y, o.k[i].z, o.k[i].w);
+    *reinterpret_cast<bf16x4 *>(Vt + (4 * dq + 0) * kVtRowH + 4 * kq) =
+        to_bf16x4(o.v[0].x, o.v[1].x, o.v[2].x, o.v[3].x);
+    *reinterpret_cast<bf16x4 *>(Vt + (4 * dq + 1) * kVtRowH + 4 * kq) =
+        to_bf16x4(o.v[0].y, o.v[1].y, o.v[2].y, o.v[3].y);
+    *reinterpret_cast<bf16x4 *>(Vt + (4 * dq + 2) * kVtRowH + 4 * kq) =
+        to_bf16x4(o.v[0].z, o.v[1].z, o.v[2].z, o.v[3].z);
+    *reinterpret_cast<bf16x4 *>(Vt + (4 * dq + 3) * kVtRowH + 4 * kq) =
+        to_bf16x4(o.v[0].w, o.v[1].w, o.v[2].w, o.v[3].w);
+}
+
+template <int D, int NTHR>
+struct TileBlocks {
+    static constexpr int UNITS = (KT / 4) * (D / 4);
+    static constexpr int PER_THREAD = (UNITS + NTHR - 1) / NTHR;
+    Block44 blk[PER_THREAD];
+};
+
+template <int D, int NTHR, bool Q8>
+__device__ __forceinline__ void fetch_tile_bf16(const PrefillParams &p, int b, int kvh, int k0, int klo, int khi,
+                                                TileBlocks<D, NTHR> &t) {
+#pragma unroll
+    for (int j = 0; j < TileBlocks<D, NTHR>::PER_THREAD; j++) {
+        const int u = threadIdx.x + j * NTHR;
+        if (u >= TileBlocks<D, NTHR>::UNITS) break;
+        const int kq = u / (D / 4);
+        const int dq = u - kq * (D / 4);
+        fetch_block44<D, Q8>(p, b, kvh, k0 + 4 * kq, 4 * dq, klo, khi, t.blk[j]);
+    }
+}
+
+template <int D, int NTHR>
+__device__ __forceinline__ void store_tile_bf16(const TileBlocks<D, NTHR> &t, __bf16 *Kh, __bf16 *Vt) {
+#pragma unroll
+    for (int j = 0; j < TileBlocks<D, NTHR>::PER_THREAD; j++) {
+        const int u = threadIdx.x + j * NTHR;
+        if (u >= TileBlocks<D, NTHR>::UNITS) break;
+        const int kq = u / (D / 4);
+        const int dq = u - kq * (D / 4);
+        store_block44<D>(t.blk[j], kq, dq, Kh, Vt);
+    }
+}
+
+template <int D, bool Q8>
+__global__ __launch_bounds__(256) void prefill_bf16_kernel(const PrefillParams p) {
+    constexpr int NW = 4, NT = 2, NTHR = 256;
+    constexpr int QW = 16 * NT;
+    constexpr int KS = D / 32;  // k-steps of S (32 dims each)
+    constexpr int DT = D / 16;  // d tiles of O
+    __shared__ __attribute__((aligned(16))) __bf16 Kh[2][KT * kKRowH<D>];
+    __shared__ __attribute__((aligned(16))) __bf16 Vt[2][D * kVtRowH];
+
+    const int b = blockIdx.z;
+    const int n_hgrp = p.group / p.hpw;
+    const int kvh = blockIdx.y / n_hgrp;
+    const int hgrp = blockIdx.y - kvh * n_hgrp;
+    const int qblk = p.n_qblocks - 1 - (int)blockIdx.x;  // longest rows first
+    const int waves_per_head = NW / p.hpw;
+    const int qwg = QW * waves_per_head;
+
+    const int row0 = p.q_start[b];
+    const int q_len = min(max(p.q_start[b + 1] - row0, 0), p.max_q_len);
+    const int pos0 = p.pos_offset[b];
+    const int qb0 = qblk * qwg;
+    if (qb0 >= q_len) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lrow = lane & 15;
+    const int lgrp = lane >> 4;
+    const int head = kvh * p.group + hgrp * p.hpw + (wave % p.hpw);
+    const int wq0 = qb0 + (wave / p.hpw) * QW;
+
+    const int q_last = min(q_len, qb0 + qwg) - 1;
+    const int khi = min(pos0 + q_last, p.pm.pos_limit - 1);
+    const int klo = window_lo(pos0 + qb0, p.sliding_window);
+
+    // Q^T operand: qb[nt][ks] = Q[query nt*16 + lrow][d = ks*32 + lgrp*8 + 0..7] as bf16
+    bf16x8 qb[NT][KS];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int lq = wq0 + nt * 16 + lrow;
+        const bool ok = lq < q_len;
+        const float *qp = p.q + ((int64_t)(row0 + (ok ? lq : 0)) * p.n_heads + head) * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const float4 a = *reinterpret_cast<const float4 *>(qp + ks * 32 + lgrp * 8);
+            const float4 c = *reinterpret_cast<const float4 *>(qp + ks * 32 + lgrp * 8 + 4);
+            const float mul = ok ? p.q_mul : 0.0f;
+            qb[nt][ks] = bf16x8{(__bf16)(a.x * mul), (__bf16)(a.y * mul), (__bf16)(a.z * mul), (__bf16)(a.w * mul),
+                                (__bf16)(c.x * mul), (__bf16)(c.y * mul), (__bf16)(c.z * mul), (__bf16)(c.w * mul)};
+        }
+    }
+
+    floatx4 o[DT][NT];
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) o[t][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[NT], lpart[NT];
+    int qpos[NT], qlo[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        m[nt] = -INFINITY;
+        lpart[nt] = 0.0f;
+        const int lq = wq0 + nt * 16 + lrow;
+        qpos[nt] = lq < q_len ? pos0 + lq : -1;
+        qlo[nt] = window_lo(pos0 + lq, p.sliding_window);
+    }
+
+    if (khi >= klo) {
+        const int kfirst = (klo / KT) * KT;
+        TileBlocks<D, NTHR> tb;
+        fetch_tile_bf16<D, NTHR, Q8>(p, b, kvh, kfirst, klo, khi, tb);
+        store_tile_bf16<D, NTHR>(tb, Kh[0], Vt[0]);
+        __syncthreads();
+        int buf = 0;
+        for (int k0 = kfirst; k0 <= khi; k0 += KT, buf ^= 1) {
+            const bool more = k0 + KT <= khi;
+            if (more) fetch_tile_bf16<D, NTHR, Q8>(p, b, kvh, k0 + KT, klo, khi, tb);
+            const __bf16 *kh = Kh[buf];
+            const __bf16 *vt = Vt[buf];
+
+            // S^T = K . Q^T
+            floatx4 sacc[2][NT];
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) sacc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                bf16x8 a[2];
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+                    a[mt] = *reinterpret_cast<const bf16x8 *>(kh + (mt * 16 + lrow) * kKRowH<D> + ks * 32 + lgrp * 8);
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++)
+                        sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt], qb[nt][ks], sacc[mt][nt], 0, 0, 0);
+            }
+
+            const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
+                                  (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
+            bf16x8 pb[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int kp = k0 + mt * 16 + 4 * lgrp + i;
+                        float x = sacc[mt][nt][i];
+                        if (p.softcap > 0.0f) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
+                        if (!interior) {
+                            const bool ok = kp <= qpos[nt] && kp >= qlo[nt] && kp >= klo && kp <= khi;
+                            x = ok ? x : -INFINITY;
+                        }
+                        sacc[mt][nt][i] = x;
+                        mx = fmaxf(mx, x);
+                    }
+                }
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const float m_new = fmaxf(m[nt], mx);
+                if (m_new == -INFINITY) {
+                    pb[nt] = bf16x8{};
+                    continue;
+                }
+                const float rs = fast_exp2(m[nt] - m_new);
+                m[nt] = m_new;
+                float pr[2][4];
+                float ls = 0.0f;
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        // the sum uses the bf16 value the MFMA multiplies
+                        const __bf16 h = (__bf16)fast_exp2(sacc[mt][nt][i] - m_new);
+                        pr[mt][i] = (float)h;
+                        ls += pr[mt][i];
+                    }
+                pb[nt] = bf16x8{(__bf16)pr[0][0], (__bf16)pr[0][1], (__bf16)pr[0][2], (__bf16)pr[0][3],
+                                (__bf16)pr[1][0], (__bf16)pr[1][1], (__bf16)pr[1][2], (__bf16)pr[1][3]};
+                lpart[nt] = lpart[nt] * rs + ls;
+                if (__ballot(rs != 1.0f)) {
+#pragma unroll
+                    for (int t = 0; t < DT; t++) o[t][nt] *= rs;
+                }
+            }
+
+            // O^T += V^T . P^T
+#pragma unroll
+            for (int t = 0; t < DT; t++) {
+                const __bf16 *vr = vt + (16 * t + lrow) * kVtRowH;
+                const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(vr + 4 * lgrp);
+                const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(vr + 16 + 4 * lgrp);
+                const bf16x8 a = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    o[t][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[nt], o[t][nt], 0, 0, 0);
+            }
+
+            if (more) store_tile_bf16<D, NTHR>(tb, Kh[buf ^ 1], Vt[buf ^ 1]);
+            __syncthreads();
+        }
+    }
+
+    // normalise and store: lane holds O^T[d = 16t + 4*lgrp + r][query lrow]
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        float lt = lpart[nt];
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
+        const int lq = wq0 + nt * 16 + lrow;
+        if (lq >= q_len) continue;
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        float *op = p.out + ((int64_t)(row0 + lq) * p.n_heads + head) * D;
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            const floatx4 v = o[t][nt] * inv;
+            *reinterpret_cast<float4 *>(op + 16 * t + 4 * lgrp) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+}
+
+template <int D, bool Q8>
+int launch_bf16(gla_ctx *ctx, const PrefillParams &prm, dim3 grid) {
+    hipLaunchKernelGGL((prefill_bf16_kernel<D, Q8>), grid, dim3(256), 0, ctx->stream, prm);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "prefill_bf16_kernel launch: %s", hipGetErrorString(e));
+    return GLA_OK;
+}
+
 template <int D, int NT, int NW, bool Q8>
 int launch_f32(gla_ctx *ctx, const PrefillParams &prm, dim3 grid) {
     hipLaunchKernelGGL((prefill_f32_kernel<D, NT, NW, Q8>), grid, dim3(NW * 64), 0, ctx->stream, prm);
@@ -429,6 +749,7 @@ int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
     default:
         return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
     }
+    if (a.precision == GLA_PREC_BF16) NT = 2, NW = 4;  // prefill_bf16_kernel's shape
     const int qwg = 16 * NT * (NW / hpw);
     PrefillParams prm;
     prm.kv = a.kv;
@@ -447,10 +768,18 @@ int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
     prm.q_mul = cap ? a.scale : a.scale * kLog2e;
     prm.softcap = cap ? a.softcap : 0.0f;
     prm.sliding_window = a.sliding_window;
-    if (a.precision != GLA_PREC_F32)
-        return set_error(GLA_ERR_INVALID, "prefill precision %d not built yet", (int)a.precision);
     if (a.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "prefill: n_seqs %d > 65535", a.n_seqs);
     dim3 grid(prm.n_qblocks, a.n_kv_heads * (group / hpw), a.n_seqs);
+    if (a.precision == GLA_PREC_BF16) {
+        switch (D) {
+        case 64:
+            return a.q8 ? launch_bf16<64, true>(ctx, prm, grid) : launch_bf16<64, false>(ctx, prm, grid);
+        case 128:
+            return a.q8 ? launch_bf16<128, true>(ctx, prm, grid) : launch_bf16<128, false>(ctx, prm, grid);
+        default:
+            return a.q8 ? launch_bf16<256, true>(ctx, prm, grid) : launch_bf16<256, false>(ctx, prm, grid);
+        }
+    }
     switch (D) {
     case 64:
         return launch_shape<64>(ctx, a.q8, prm, grid);

@@ -9,6 +9,13 @@ import numpy as np
 ABS_TOL = 1e-4
 REL_TOL = 1e-3
 
+# bf16-input prefill (Q, K, V and the probabilities rounded to bf16, 8
+# significant bits; fp32 accumulation): scores carry ~sqrt(d) * 2^-8 relative
+# error and each P.V term ~2^-8, so outputs of N(0,1) data move by ~1e-3 to
+# 1e-2. Bar: max abs 3e-2 or rel 3e-2 per element.
+BF16_ABS_TOL = 3e-2
+BF16_REL_TOL = 3e-2
+
 
 def attention_f64(q, K, V, scale, softcap=None):
     """q [d], K/V [L][d] -> softmax(cap(q.K*scale)).V in float64."""

@@ -1,6 +1,7 @@
-"""Batched causal prefill on the GPU (fp32 MFMA) through the C ABI, against the
-oracle's prefill loop (src/transformer/forward.rs:927-958).
-fp32 bar: max abs 1e-4 / rel 1e-3; indexing bit-exact."""
+"""Batched causal prefill on the GPU (fp32 MFMA and the bf16-input variant) through the C ABI,
+against the oracle's prefill loop (src/transformer/forward.rs:927-958).
+fp32 bar: max abs 1e-4 / rel 1e-3; bf16 bar: max abs 3e-2 / rel 3e-2 (helpers.BF16_*);
+indexing bit-exact for both (K = 0, small-integer V: every bf16 rounding is exact)."""
 from __future__ import annotations
 
 import numpy as np
@@ -9,7 +10,7 @@ import pytest
 import oracle as orc
 from glint_amd import synth
 from gpu_util import Contig, Pool, run_prefill
-from helpers import assert_close
+from helpers import BF16_ABS_TOL, BF16_REL_TOL, assert_close, max_errors
 
 pytestmark = pytest.mark.gpu
 
@@ -58,7 +59,31 @@ def test_prefill_paged(backend, dtype):
             assert_close(got[rows], want, what=f"paged {dtype} seq {b} window {window}")
 
 
-def test_prefill_indexing_is_bit_exact(backend):
+@pytest.mark.parametrize("d,H,Hkv", [(128, 8, 2), (64, 9, 3), (256, 4, 2), (128, 4, 4)])
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+def test_prefill_bf16_varlen_batch(backend, dtype, d, H, Hkv):
+    """bf16-input variant over the varlen batch (chunked offsets, soft-cap, windows): within the
+    bf16 bar of the fp32 oracle, and really rounded (not equal to the fp32 kernel's output)."""
+    lens = [70, 1, 130]
+    offs = [0, 40, 17]
+    max_seq = max(o + n for o, n in zip(offs, lens))
+    c = Contig(backend, dtype, 3, 2, max_seq, Hkv, d, seed=850 + d + H)
+    q = synth.normal(950 + d, (sum(lens), H, d))
+    q_start = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    scale = 1 / np.sqrt(d)
+    for layer, cap, window in [(0, None, None), (1, 30.0, None), (0, None, 21), (1, 15.0, 64)]:
+        got = run_prefill(backend, c.cache, q, q_start, offs, H, scale, cap, window, layer=layer, precision="bf16")
+        f32 = run_prefill(backend, c.cache, q, q_start, offs, H, scale, cap, window, layer=layer)
+        assert max_errors(got, f32)[0] > 0.0, "bf16 variant returned the fp32 result"
+        for b in range(3):
+            rows = slice(q_start[b], q_start[b + 1])
+            want = _oracle_prefill(c.stores[b], q[rows], offs[b], H, Hkv, d, scale, cap, window, layer)
+            assert_close(got[rows], want, BF16_ABS_TOL, BF16_REL_TOL,
+                         what=f"bf16 {dtype} d{d} H{H}/{Hkv} seq{b} layer{layer} cap{cap} w{window}")
+
+
+@pytest.mark.parametrize("precision", ["f32", "bf16"])
+def test_prefill_indexing_is_bit_exact(backend, precision):
     """K = 0 and small-integer V: out = mean of V over [window(pos), pos] exactly."""
     H, Hkv, d = 8, 2, 64
     kv_dim = Hkv * d
@@ -69,7 +94,7 @@ def test_prefill_indexing_is_bit_exact(backend):
     c = Contig(backend, "f32", 1, 1, T, Hkv, d, k=np.zeros_like(v), v=v)
     q = synth.normal(4, (T, H, d))
     for window in (None, 16, 33):
-        got = run_prefill(backend, c.cache, q, [0, T], [0], H, 0.125, None, window)
+        got = run_prefill(backend, c.cache, q, [0, T], [0], H, 0.125, None, window, precision=precision)
         for pos in range(T):
             lo = 0 if not window else max(0, pos - window + 1)
             s = v[0, 0, lo:pos + 1].astype(np.float64).sum(0).astype(np.float32)
@@ -77,10 +102,11 @@ def test_prefill_indexing_is_bit_exact(backend):
             for h in range(H):
                 kvh = h // (H // Hkv)
                 assert np.array_equal(got[pos, h].view(np.uint32), want[kvh * d:(kvh + 1) * d].view(np.uint32)), \
-                    (window, pos, h)
+                    (precision, window, pos, h)
 
 
-def test_cfg4_llama_prefill_4x2048(backend):
+@pytest.mark.parametrize("precision", ["f32", "bf16"])
+def test_cfg4_llama_prefill_4x2048(backend, precision):
     """BASELINE config 4 at full size (4 prompts x 2048, H32/KV8, d128, f32 KV cache), every
     16th query row of each prompt against the oracle."""
     H, Hkv, d, S, B = 32, 8, 128, 2048, 4
@@ -88,7 +114,8 @@ def test_cfg4_llama_prefill_4x2048(backend):
     q = synth.normal(4005, (B * S, H, d))
     q_start = np.arange(B + 1, dtype=np.int32) * S
     scale = 1 / np.sqrt(128)
-    got = run_prefill(backend, c.cache, q, q_start, [0] * B, H, scale)
+    got = run_prefill(backend, c.cache, q, q_start, [0] * B, H, scale, precision=precision)
+    tol = (BF16_ABS_TOL, BF16_REL_TOL) if precision == "bf16" else ()
     for b in range(B):
         rows = np.arange(b * S, (b + 1) * S)
         sel = np.arange(b % 16, S, 16)
@@ -96,4 +123,4 @@ def test_cfg4_llama_prefill_4x2048(backend):
         for i, lp in enumerate(sel):
             out[i] = orc.attn_heads_cpu(q[b * S + lp].reshape(-1), c.stores[b], 0, 0, lp + 1, H, H // Hkv, d,
                                         scale).reshape(H, d)
-        assert_close(got[rows[sel]], out, what=f"cfg4 prompt {b}")
+        assert_close(got[rows[sel]], out, *tol, what=f"cfg4 {precision} prompt {b}")
