@@ -6,6 +6,7 @@
 Outputs (in-tree, git-ignored, shipped with the tree to the GPU box):
     glint_amd/libglint_attn.so    HIP kernels + C ABI (include/glint_attn.h)
     glint_amd/libglint_synth.so   seeded synthetic inputs (host C)
+    glint_amd/libglint_probe.so   achievable-peak probes for bench.py (stream read, MFMA loops)
     oracle/liboracle.so           CPU oracle, built by oracle/Makefile (tests only)
 """
 from __future__ import annotations
@@ -22,6 +23,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 HIP_LIB = PKG / "libglint_attn.so"
 SYNTH_LIB = PKG / "libglint_synth.so"
+PROBE_LIB = PKG / "libglint_probe.so"
 ORACLE_DIR = ROOT / "oracle"
 ORACLE_LIB = ORACLE_DIR / "liboracle.so"
 
@@ -66,6 +68,13 @@ def build_hip(jobs: int = 4) -> Path:
     return HIP_LIB
 
 
+def build_probe() -> Path:
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, *HIP_FLAGS, "-shared", "-o", str(tmp), str(CSRC / "gla_probe.hip")])
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
 def build_synth() -> Path:
     tmp = SYNTH_LIB.with_suffix(".so.tmp")
     _run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-Wall", "-o", str(tmp), str(CSRC / "synth.c"),
@@ -83,6 +92,7 @@ def build_all(jobs: int = 4) -> None:
     build_synth()
     build_oracle()
     build_hip(jobs)
+    build_probe()
 
 
 if __name__ == "__main__":
@@ -94,4 +104,5 @@ if __name__ == "__main__":
         build_oracle()
     else:
         build_all()
-    print("built:", ", ".join(str(p.relative_to(ROOT)) for p in (HIP_LIB, SYNTH_LIB, ORACLE_LIB) if p.exists()))
+    print("built:", ", ".join(str(p.relative_to(ROOT)) for p in (HIP_LIB, SYNTH_LIB, PROBE_LIB, ORACLE_LIB)
+                               if p.exists()))

@@ -1,0 +1,134 @@
+// gla_probe.hip -- achievable-peak probes for the benchmark (not part of the
+// attention ABI): a streaming HBM read and MFMA-only loops, timed with HIP
+// events on the null stream. bench.py reports each kernel's throughput both
+// against MI355X's published peaks and against these measured ceilings.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Grid-stride read of n 16-byte units with non-temporal loads (the decode
+// kernels' load kind); the XOR keeps the loads alive.
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4 *a, size_t n, uint32_t *sink) {
+    uint32_t acc = 0;
+    const size_t stride = (size_t)gridDim.x * 256 * 4;
+    for (size_t i = blockIdx.x * (size_t)1024 + threadIdx.x; i < n; i += stride) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            size_t j = i + (size_t)u * 256;
+            j = j < n ? j : i;
+            v[u] = __builtin_nontemporal_load(a + j);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+// MFMA-only loops: 8 independent accumulators per wave, `iters` rounds.
+__global__ __launch_bounds__(256) void mfma_f32_kernel(int iters, float *sink) {
+    floatx4 c[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) c[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const float a = 1.0f + threadIdx.x * 1e-7f, b = 1.0f - threadIdx.x * 1e-7f;
+    for (int it = 0; it < iters; it++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) c[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c[j], 0, 0, 0);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) s += c[j][0] + c[j][1] + c[j][2] + c[j][3];
+    if (s == 12345.0f) sink[0] = s;
+}
+
+__global__ __launch_bounds__(256) void mfma_bf16_kernel(int iters, float *sink) {
+    floatx4 c[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) c[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8 a, b;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        a[k] = (__bf16)(1.0f + (threadIdx.x + k) * 1e-3f);
+        b[k] = (__bf16)(1.0f - (threadIdx.x + k) * 1e-3f);
+    }
+    for (int it = 0; it < iters; it++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) c[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c[j], 0, 0, 0);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) s += c[j][0] + c[j][1] + c[j][2] + c[j][3];
+    if (s == 12345.0f) sink[0] = s;
+}
+
+template <typename F>
+int time_ms(F launch, int reps, float *ms_out) {
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -2;
+    launch();  // warm-up
+    if (hipDeviceSynchronize() != hipSuccess) return -4;
+    hipEventRecord(e0, nullptr);
+    for (int i = 0; i < reps; i++) launch();
+    hipEventRecord(e1, nullptr);
+    if (hipEventSynchronize(e1) != hipSuccess) return -4;
+    float ms = 0.0f;
+    hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    *ms_out = ms / reps;
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Read `bytes` (a multiple of 16) from device buffer `buf`; GB/s of one pass.
+int glp_stream_read(const void *buf, size_t bytes, int reps, double *gbs_out) {
+    uint32_t *sink = nullptr;
+    if (hipMalloc(&sink, 4) != hipSuccess) return -3;
+    int n_cu = 0;
+    hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, 0);
+    const size_t n = bytes / 16;
+    float ms = 0.0f;
+    const int rc = time_ms(
+        [&] {
+            hipLaunchKernelGGL(stream_read_kernel, dim3(n_cu * 16), dim3(256), 0, nullptr,
+                               static_cast<const u32x4 *>(buf), n, sink);
+        },
+        reps, &ms);
+    hipFree(sink);
+    if (rc != 0) return rc;
+    *gbs_out = (double)bytes / (ms * 1e-3) / 1e9;
+    return 0;
+}
+
+// kind 0: v_mfma_f32_16x16x4_f32, kind 1: v_mfma_f32_16x16x32_bf16, on 8
+// waves per CU; TFLOP/s.
+int glp_mfma_peak(int kind, int iters, double *tflops_out) {
+    float *sink = nullptr;
+    if (hipMalloc(&sink, 4) != hipSuccess) return -3;
+    int n_cu = 0;
+    hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, 0);
+    const dim3 grid(n_cu * 2), block(256);
+    float ms = 0.0f;
+    int rc;
+    double flops_per_mfma;
+    if (kind == 0) {
+        rc = time_ms([&] { hipLaunchKernelGGL(mfma_f32_kernel, grid, block, 0, nullptr, iters, sink); }, 3, &ms);
+        flops_per_mfma = 16.0 * 16 * 4 * 2;
+    } else {
+        rc = time_ms([&] { hipLaunchKernelGGL(mfma_bf16_kernel, grid, block, 0, nullptr, iters, sink); }, 3, &ms);
+        flops_per_mfma = 16.0 * 16 * 32 * 2;
+    }
+    hipFree(sink);
+    if (rc != 0) return rc;
+    const double waves = (double)grid.x * 4;
+    *tflops_out = waves * iters * 8 * flops_per_mfma / (ms * 1e-3) / 1e12;
+    return 0;
+}
+
+}  // extern "C"
