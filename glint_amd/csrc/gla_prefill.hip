@@ -175,11 +175,15 @@ __global__ __launch_bounds__(NW * 64) void prefill_f32_kernel(const PrefillParam
     __shared__ __attribute__((aligned(16))) float Ks[2][KT * kRow<D>];
     __shared__ __attribute__((aligned(16))) float Vs[2][KT * kRow<D>];
 
-    const int b = blockIdx.z;
+    // grid (sequence x KV head x head group, query block): every unit's
+    // longest (last) query block is dispatched before any shorter one, so the
+    // grid ends on short workgroups
     const int n_hgrp = p.group / p.hpw;
-    const int kvh = blockIdx.y / n_hgrp;
-    const int hgrp = blockIdx.y - kvh * n_hgrp;
-    const int qblk = p.n_qblocks - 1 - (int)blockIdx.x;  // longest rows first
+    const int unit = blockIdx.x;
+    const int b = unit / (p.n_kv_heads * n_hgrp);
+    const int kvh = (unit - b * p.n_kv_heads * n_hgrp) / n_hgrp;
+    const int hgrp = unit - (b * p.n_kv_heads + kvh) * n_hgrp;
+    const int qblk = p.n_qblocks - 1 - (int)blockIdx.y;
     const int waves_per_head = NW / p.hpw;
     const int qwg = QW * waves_per_head;
 
@@ -512,11 +516,15 @@ __global__ __launch_bounds__(256) void prefill_bf16_kernel(const PrefillParams p
     __shared__ __attribute__((aligned(16))) __bf16 Kh[2][KT * kKRowH<D>];
     __shared__ __attribute__((aligned(16))) __bf16 Vt[2][D * kVtRowH];
 
-    const int b = blockIdx.z;
+    // grid (sequence x KV head x head group, query block): every unit's
+    // longest (last) query block is dispatched before any shorter one, so the
+    // grid ends on short workgroups
     const int n_hgrp = p.group / p.hpw;
-    const int kvh = blockIdx.y / n_hgrp;
-    const int hgrp = blockIdx.y - kvh * n_hgrp;
-    const int qblk = p.n_qblocks - 1 - (int)blockIdx.x;  // longest rows first
+    const int unit = blockIdx.x;
+    const int b = unit / (p.n_kv_heads * n_hgrp);
+    const int kvh = (unit - b * p.n_kv_heads * n_hgrp) / n_hgrp;
+    const int hgrp = unit - (b * p.n_kv_heads + kvh) * n_hgrp;
+    const int qblk = p.n_qblocks - 1 - (int)blockIdx.y;
     const int waves_per_head = NW / p.hpw;
     const int qwg = QW * waves_per_head;
 
@@ -768,8 +776,8 @@ int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
     prm.q_mul = cap ? a.scale : a.scale * kLog2e;
     prm.softcap = cap ? a.softcap : 0.0f;
     prm.sliding_window = a.sliding_window;
-    if (a.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "prefill: n_seqs %d > 65535", a.n_seqs);
-    dim3 grid(prm.n_qblocks, a.n_kv_heads * (group / hpw), a.n_seqs);
+    if (prm.n_qblocks > 65535) return set_error(GLA_ERR_INVALID, "prefill: %d query blocks > 65535", prm.n_qblocks);
+    dim3 grid(a.n_seqs * a.n_kv_heads * (group / hpw), prm.n_qblocks, 1);
     if (a.precision == GLA_PREC_BF16) {
         switch (D) {
         case 64:
