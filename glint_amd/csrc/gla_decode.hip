@@ -63,6 +63,28 @@ __device__ __forceinline__ float sum8(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// x combined with lane ^ 8 / ^ 16 / ^ 32 on the VALU (DPP row rotation and the
+// gfx950 row swaps), no LDS round trip: the merge of the 8 lane groups.
+__device__ __forceinline__ float other8(float x) {  // lane ^ 8 within a row of 16
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float add16(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+__device__ __forceinline__ float add32(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+__device__ __forceinline__ float max16(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ __forceinline__ float max32(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+
 // tanh(x) = sign(x) (1 - t) / (1 + t), t = exp(-2|x|).
 __device__ __forceinline__ float tanh_approx(float x) {
     float t = fast_exp2(-2.0f * kLog2e * fabsf(x));
@@ -267,20 +289,14 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
 #pragma unroll
     for (int g = 0; g < GT; g++) {
         float M = m[g];
-        M = fmaxf(M, __shfl_xor(M, 8));
-        M = fmaxf(M, __shfl_xor(M, 16));
-        M = fmaxf(M, __shfl_xor(M, 32));
+        M = max32(max16(fmaxf(M, other8(M))));
         const float f = (m[g] == -INFINITY) ? 0.0f : fast_exp2(m[g] - M);
         float lg = l[g] * f;
-        lg += __shfl_xor(lg, 8);
-        lg += __shfl_xor(lg, 16);
-        lg += __shfl_xor(lg, 32);
+        lg = add32(add16(lg + other8(lg)));
 #pragma unroll
         for (int e = 0; e < EPL; e++) {
             float a = acc[g][e] * f;
-            a += __shfl_xor(a, 8);
-            a += __shfl_xor(a, 16);
-            a += __shfl_xor(a, 32);
+            a = add32(add16(a + other8(a)));
             acc[g][e] = a;
         }
         m[g] = M;
