@@ -48,6 +48,21 @@ struct PrefillParams {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max / sum over the four 16-lane rows (lane ^ 16, lane ^ 32) with the gfx950
+// row swaps: VALU only, no LDS round trip.
+__device__ __forceinline__ float max_rows4(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+__device__ __forceinline__ float sum_rows4(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
+
 __device__ __forceinline__ float tanh_approx(float x) {
     float t = fast_exp2(-2.0f * kLog2e * fabsf(x));
     float r = (1.0f - t) / (1.0f + t);
@@ -304,8 +319,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_f32_kernel(const PrefillParam
                         mx = fmaxf(mx, x);
                     }
                 }
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                mx = max_rows4(mx);
                 const float m_new = fmaxf(m[nt], mx);
                 if (m_new == -INFINITY) {
 #pragma unroll
@@ -364,8 +378,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_f32_kernel(const PrefillParam
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         float lt = lpart[nt];
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
+        lt = sum_rows4(lt);
         const int lq = wq0 + nt * 16 + lrow;
         if (lq >= q_len) continue;
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
@@ -632,8 +645,7 @@ __global__ __launch_bounds__(256) void prefill_bf16_kernel(const PrefillParams p
                         mx = fmaxf(mx, x);
                     }
                 }
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                mx = max_rows4(mx);
                 const float m_new = fmaxf(m[nt], mx);
                 if (m_new == -INFINITY) {
                     pb[nt] = bf16x8{};
@@ -682,8 +694,7 @@ __global__ __launch_bounds__(256) void prefill_bf16_kernel(const PrefillParams p
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         float lt = lpart[nt];
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
+        lt = sum_rows4(lt);
         const int lq = wq0 + nt * 16 + lrow;
         if (lq >= q_len) continue;
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
