@@ -7,6 +7,8 @@ Outputs (in-tree, git-ignored, shipped with the tree to the GPU box):
     glint_amd/libglint_attn.so    HIP kernels + C ABI (include/glint_attn.h)
     glint_amd/libglint_synth.so   seeded synthetic inputs (host C)
     glint_amd/libglint_probe.so   achievable-peak probes for bench.py (stream read, MFMA loops)
+    glint_amd/libglint_host.so    C++ host layer over the C ABI (glint_amd/host/glint.hpp)
+    glint_amd/_build/test_host    its test program (tests/cpp/test_host.cpp; run by tests/test_host_cpp.py)
     oracle/liboracle.so           CPU oracle, built by oracle/Makefile (tests only)
 """
 from __future__ import annotations
@@ -24,6 +26,8 @@ BUILD = PKG / "_build"
 HIP_LIB = PKG / "libglint_attn.so"
 SYNTH_LIB = PKG / "libglint_synth.so"
 PROBE_LIB = PKG / "libglint_probe.so"
+HOST_LIB = PKG / "libglint_host.so"
+HOST_TEST = BUILD / "test_host"
 ORACLE_DIR = ROOT / "oracle"
 ORACLE_LIB = ORACLE_DIR / "liboracle.so"
 
@@ -75,6 +79,27 @@ def build_probe() -> Path:
     return PROBE_LIB
 
 
+HOST_FLAGS = ["-O2", "-std=c++17", "-Wall", "-Wextra", "-fPIC", f"-I{ROOT / 'include'}", f"-I{PKG / 'host'}"]
+
+
+def build_host() -> Path:
+    """The C++ host layer (links libglint_attn.so, found next to it at run time)."""
+    tmp = HOST_LIB.with_suffix(".so.tmp")
+    _run(["g++", *HOST_FLAGS, "-shared", "-o", str(tmp), str(PKG / "host" / "glint.cpp"), f"-L{PKG}",
+          "-lglint_attn", "-Wl,-rpath,$ORIGIN", "-Wl,--allow-shlib-undefined"])
+    os.replace(tmp, HOST_LIB)
+    return HOST_LIB
+
+
+def build_host_tests() -> Path:
+    BUILD.mkdir(exist_ok=True)
+    tmp = HOST_TEST.with_suffix(".tmp")
+    _run(["g++", *HOST_FLAGS, f"-I{ROOT / 'tests' / 'cpp'}", "-o", str(tmp), str(ROOT / "tests" / "cpp" / "test_host.cpp"),
+          f"-L{PKG}", "-lglint_host", "-lglint_attn", "-Wl,-rpath,$ORIGIN/..", "-Wl,--allow-shlib-undefined"])
+    os.replace(tmp, HOST_TEST)
+    return HOST_TEST
+
+
 def build_synth() -> Path:
     tmp = SYNTH_LIB.with_suffix(".so.tmp")
     _run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-Wall", "-o", str(tmp), str(CSRC / "synth.c"),
@@ -93,16 +118,22 @@ def build_all(jobs: int = 4) -> None:
     build_oracle()
     build_hip(jobs)
     build_probe()
+    build_host()
+    build_host_tests()
 
 
 if __name__ == "__main__":
     args = set(sys.argv[1:])
     if "--hip" in args:
         build_hip()
+    elif "--cpp" in args:
+        build_host()
+        build_host_tests()
     elif "--host" in args:
         build_synth()
         build_oracle()
     else:
         build_all()
-    print("built:", ", ".join(str(p.relative_to(ROOT)) for p in (HIP_LIB, SYNTH_LIB, PROBE_LIB, ORACLE_LIB)
+    print("built:", ", ".join(str(p.relative_to(ROOT)) for p in (HIP_LIB, SYNTH_LIB, PROBE_LIB, HOST_LIB,
+                                                                      HOST_TEST, ORACLE_LIB)
                                if p.exists()))
