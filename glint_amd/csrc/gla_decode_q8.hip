@@ -61,6 +61,9 @@ constexpr int kWaves = 4;
 constexpr int kGT = 4;  // q-heads per wave
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxChunks = 64;  // preferred bound on chunks per unit
+// Workgroup rows listed in the launch arguments (see Q8Params::rows): 3 KB of
+// the 4 KB kernel-argument limit.
+constexpr int kMaxRows = 1536;
 
 struct Q8Params {
     const uint8_t *base;  // KV storage; a (page, head) block is 34*D bytes
@@ -81,6 +84,12 @@ struct Q8Params {
     int max_len;
     float q_mul;    // scale*log2(e), or scale with a soft-cap
     float softcap;  // > 0: cap * tanh(s / cap)
+    // With the host lengths known: the (sequence, workgroup) of grid row y,
+    // seq << 6 | wg, longest workgroups first, and no rows for workgroups
+    // past a sequence's end (n_rows > 0; grid (units, n_rows, 1)). Else
+    // n_rows = 0 and the grid is (units, max_wg, n_seqs).
+    int n_rows;
+    uint16_t rows[kMaxRows];
 };
 
 struct Range {
@@ -708,7 +717,15 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
     // head index runs fastest, so the workgroups reading the 8 head spans of
     // the same pages are dispatched together and the DRAM rows those pages
     // open are read out while open (measured ~25% over chunk-fastest order)
-    const int b = blockIdx.z;
+    int b, wg;
+    if (p.n_rows > 0) {
+        const int e = p.rows[blockIdx.y];
+        b = e >> 6;
+        wg = e & 63;
+    } else {
+        b = blockIdx.z;
+        wg = blockIdx.y;
+    }
     const int kvh = blockIdx.x / p.n_hg;
     const int hg = blockIdx.x - kvh * p.n_hg;
     const int g0 = hg * kGT;
@@ -718,7 +735,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
 
     const Range r = seq_range(p, b);
     if (r.n_pages == 0) {  // empty window: zero output (the reference's pre-zeroed buffer)
-        if (blockIdx.y == 0)
+        if (wg == 0)
             for (int idx = tid; idx < gcount * D; idx += kThreads) out[idx] = 0.0f;
         return;
     }
@@ -728,7 +745,6 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
     // working while the others wait at the merge.
     const int span = kWaves * p.ch;
     const int n_wg = (r.n_pages + span - 1) / span;
-    const int wg = blockIdx.y;
     if (wg >= n_wg) return;
     const int wg_pages = min(span, r.n_pages - wg * span);
     const int per_wave = ((wg_pages + 2 * kWaves - 1) / (2 * kWaves)) * 2;  // even: a step is two pages
@@ -834,12 +850,12 @@ __global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p
 }
 
 template <int D>
-int launch_d(gla_ctx *ctx, const Q8Params &prm, dim3 grid) {
+int launch_d(gla_ctx *ctx, const Q8Params &prm, dim3 grid, int n_seqs) {
     hipLaunchKernelGGL((decode_q8_mfma_kernel<D>), grid, dim3(kWaves * 64), 0, ctx->stream, prm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "decode_q8_mfma_kernel launch: %s", hipGetErrorString(e));
     if (prm.max_wg > 1) {
-        hipLaunchKernelGGL((decode_q8_combine_kernel<D>), dim3(kGT * D / 256, grid.x, grid.z), dim3(256), 0,
+        hipLaunchKernelGGL((decode_q8_combine_kernel<D>), dim3(kGT * D / 256, grid.x, n_seqs), dim3(256), 0,
                            ctx->stream, prm);
         e = hipGetLastError();
         if (e != hipSuccess)
@@ -952,13 +968,33 @@ int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
     if (d.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "decode: n_seqs %d > 65535", d.n_seqs);
     if (max_wg > 65535) return set_error(GLA_ERR_INVALID, "decode: %lld workgroups per sequence > 65535", (long long)max_wg);
     dim3 grid(d.n_kv_heads * n_hg, (unsigned)max_wg, d.n_seqs);
+    // With the host lengths, list the workgroups that have pages (plus one per
+    // empty window, which zeroes its output), longest first: the dispatcher
+    // then starts the full workgroups before the short last ones of each
+    // sequence, which fill in at the end.
+    prm.n_rows = 0;
+    if (!np.empty() && max_wg <= 64 && d.n_seqs <= 1024) {
+        const int span = kWaves * (int)ch;
+        std::vector<std::pair<int, uint16_t>> w;
+        w.reserve(kMaxRows + 1);
+        for (int b = 0; b < d.n_seqs && w.size() <= (size_t)kMaxRows; b++) {
+            if (np[b] == 0) w.push_back({0, (uint16_t)(b << 6)});
+            for (int j = 0; j * span < np[b]; j++) w.push_back({std::min(span, np[b] - j * span), (uint16_t)(b << 6 | j)});
+        }
+        if (w.size() <= (size_t)kMaxRows) {
+            std::stable_sort(w.begin(), w.end(), [](const auto &x, const auto &y) { return x.first > y.first; });
+            for (size_t i = 0; i < w.size(); i++) prm.rows[i] = w[i].second;
+            prm.n_rows = (int)w.size();
+            grid = dim3(d.n_kv_heads * n_hg, (unsigned)w.size(), 1);
+        }
+    }
     switch (D) {
     case 64:
-        return launch_d<64>(ctx, prm, grid);
+        return launch_d<64>(ctx, prm, grid, d.n_seqs);
     case 128:
-        return launch_d<128>(ctx, prm, grid);
+        return launch_d<128>(ctx, prm, grid, d.n_seqs);
     case 256:
-        return launch_d<256>(ctx, prm, grid);
+        return launch_d<256>(ctx, prm, grid, d.n_seqs);
     }
     return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
 }
