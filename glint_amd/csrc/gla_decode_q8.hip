@@ -895,8 +895,9 @@ int host_seq_pages(int start, int len, int max_len, int pos_limit) {
 // With the pages of every sequence known (np) the counts are exact; without
 // them every sequence is taken to span max_pages.
 int choose_chunk_pages(const std::vector<int> &np, int n_seqs, int max_pages, int n_hu, int64_t slots) {
-    const int lo = std::max(2, (max_pages + kMaxChunks - 1) / kMaxChunks);
-    int ch = std::max(20, (lo + 1) & ~1);
+    // at most 64 pages per wave (one page id per lane), even past kMaxChunks chunks
+    const int lo = std::min(64, std::max(2, (max_pages + kMaxChunks - 1) / kMaxChunks));
+    int ch = std::min(64, std::max(20, (lo + 1) & ~1));
     for (; ch > 2 && ch - 2 >= lo; ch -= 2) {
         int64_t wgs = 0;
         if (np.empty()) {

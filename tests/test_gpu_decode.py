@@ -118,6 +118,23 @@ def test_q8_chunk_sizes(backend, monkeypatch, chunk, host_lengths):
     assert_close(got, want, what=f"q8 chunk {chunk}")
 
 
+@pytest.mark.parametrize("host_lengths", [True, False])
+def test_q8_context_beyond_64_chunks(backend, monkeypatch, host_lengths):
+    """A 70,000-token window (4,376 pages, more than 64 chunks of 64 pages): chunks stay at
+    most 64 pages, one page id per lane, with more workgroups per sequence instead. A
+    short sequence beside it keeps the launch ragged."""
+    monkeypatch.delenv("GLA_Q8_CHUNK_PAGES", raising=False)
+    H, Hkv, d = 8, 2, 64
+    ctx = np.array([70000, 300], np.int32)
+    pb = synth.paged_batch(821, ctx)
+    p = Pool(backend, "q8", pb, Hkv, d, seed=822)
+    q = synth.normal(823, (len(ctx), H, d))
+    want = _oracle_decode(p.stores, q, pb.kv_start, pb.kv_len, H, Hkv, d, 0.125)
+    got = run_decode(backend, p.pool, q, pb.kv_start, pb.kv_len, H, 0.125, table=pb.table,
+                     host_lengths=host_lengths)
+    assert_close(got, want, what="q8 70k context")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "q8"])
 @pytest.mark.parametrize("paged", [False, True])
 def test_indexing_is_bit_exact(backend, dtype, paged):
