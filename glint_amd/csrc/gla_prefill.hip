@@ -520,9 +520,15 @@ __device__ __forceinline__ void store_tile_bf16(const TileBlocks<D, NTHR> &t, __
     }
 }
 
+// Waves per workgroup of the bf16 kernel (32 queries each): 8 share each
+// staged K/V tile (d = 256: 4, whose registers need the 512-VGPR budget of
+// one wave per SIMD).
+template <int D>
+constexpr int kBf16Waves = D == 256 ? 4 : 8;
+
 template <int D, bool Q8>
-__global__ __launch_bounds__(256) void prefill_bf16_kernel(const PrefillParams p) {
-    constexpr int NW = 4, NT = 2, NTHR = 256;
+__global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const PrefillParams p) {
+    constexpr int NW = kBf16Waves<D>, NT = 2, NTHR = NW * 64;
     constexpr int QW = 16 * NT;
     constexpr int KS = D / 32;  // k-steps of S (32 dims each)
     constexpr int DT = D / 16;  // d tiles of O
@@ -709,7 +715,7 @@ __global__ __launch_bounds__(256) void prefill_bf16_kernel(const PrefillParams p
 
 template <int D, bool Q8>
 int launch_bf16(gla_ctx *ctx, const PrefillParams &prm, dim3 grid) {
-    hipLaunchKernelGGL((prefill_bf16_kernel<D, Q8>), grid, dim3(256), 0, ctx->stream, prm);
+    hipLaunchKernelGGL((prefill_bf16_kernel<D, Q8>), grid, dim3(kBf16Waves<D> * 64), 0, ctx->stream, prm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "prefill_bf16_kernel launch: %s", hipGetErrorString(e));
     return GLA_OK;
@@ -768,7 +774,8 @@ int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
     default:
         return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
     }
-    if (a.precision == GLA_PREC_BF16) NT = 2, NW = 4;  // prefill_bf16_kernel's shape
+    if (a.precision == GLA_PREC_BF16)  // prefill_bf16_kernel's shape
+        NT = 2, NW = D == 256 ? kBf16Waves<256> : kBf16Waves<128>;
     const int qwg = 16 * NT * (NW / hpw);
     PrefillParams prm;
     prm.kv = a.kv;
