@@ -422,8 +422,10 @@ template <int D, bool Q8>
 __device__ __forceinline__ void fetch_block44(const PrefillParams &p, int b, int kvh, int key0, int d0, int klo,
                                               int khi, Block44 &o) {
     const int64_t head_off = (int64_t)kvh * p.kv.head_stride;
-    // key0 is a multiple of 4, so the 4 keys share one page
-    const int64_t pid = map_page(p.pm, b, key0 >> 4);
+    // key0 is a multiple of 4, so the 4 keys share one page; a block past
+    // khi (zeroed below) looks up khi's page, so the page-table read stays
+    // inside the sequence's row
+    const int64_t pid = map_page(p.pm, b, min(key0, max(khi, 0)) >> 4);
     if constexpr (Q8) {
         const int64_t hb = pid * p.kv.page_stride + head_off;
         const int slot0 = key0 & 15;
@@ -713,6 +715,323 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Staged bf16 path: a pre-pass converts each (sequence, KV head, 32-key tile)
+// the prefill reads to bf16 once, in the exact LDS image the MFMA operand
+// reads want, and the main kernel copies tile images into an LDS ring with
+// direct global->LDS loads (no registers, no conversion, three tiles ahead).
+// The image of a tile is 128*D bytes, 16-byte pieces:
+//   K: piece ((mt*(D/8) + c)*16 + r) = K[key mt*16 + r][dims 8c .. 8c+7]
+//   V: piece ((t*4 + g)*16 + r)      = V[keys 4g..4g+3, 16+4g..16+4g+3][dim 16t + r]
+// so the 16 lanes of each read pass (r = 0..15) take 16 consecutive pieces
+// of one 256-byte line: no LDS bank conflicts, and the whole image is one
+// contiguous copy. Keys outside the sequence's window union [window_lo(pos0),
+// last query] are zero, as the in-kernel staging zeroes them.
+constexpr int kRingTiles = 4;
+
+template <int D>
+constexpr int kTileImage = 128 * D;
+
+template <int D, bool Q8>
+__global__ __launch_bounds__(256) void stage_bf16_kernel(const PrefillParams p, uint8_t *img, int n_tiles) {
+    const int t = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int b = blockIdx.z;
+    const int row0 = p.q_start[b];
+    const int q_len = min(max(p.q_start[b + 1] - row0, 0), p.max_q_len);
+    if (q_len == 0) return;
+    const int pos0 = p.pos_offset[b];
+    const int khi = min(pos0 + q_len - 1, p.pm.pos_limit - 1);
+    const int klo = window_lo(pos0, p.sliding_window);
+    const int k0 = t * KT;
+    if (khi < klo || k0 > khi || k0 + KT - 1 < klo) return;  // a tile no query of the sequence reads
+
+    __shared__ __attribute__((aligned(16))) float Kf[KT][D + 4];
+    __shared__ __attribute__((aligned(16))) float Vf[KT][D + 4];
+    for (int u = threadIdx.x; u < (KT / 4) * (D / 4); u += 256) {
+        const int kq = u / (D / 4);
+        const int dq = u - kq * (D / 4);
+        Block44 blk;
+        fetch_block44<D, Q8>(p, b, kvh, k0 + 4 * kq, 4 * dq, klo, khi, blk);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            *reinterpret_cast<float4 *>(&Kf[4 * kq + i][4 * dq]) = blk.k[i];
+            *reinterpret_cast<float4 *>(&Vf[4 * kq + i][4 * dq]) = blk.v[i];
+        }
+    }
+    __syncthreads();
+    uint8_t *dst = img + (((int64_t)b * p.n_kv_heads + kvh) * n_tiles + t) * kTileImage<D>;
+    constexpr int NP = 4 * D;  // pieces of K (and of V) per tile
+    for (int i = threadIdx.x; i < NP; i += 256) {
+        const int mt = i / (D / 8 * 16);
+        const int rem = i - mt * (D / 8 * 16);
+        const int c = rem >> 4;
+        const int key = mt * 16 + (rem & 15);
+        const float *kr = &Kf[key][8 * c];
+        const bf16x8 h = bf16x8{(__bf16)kr[0], (__bf16)kr[1], (__bf16)kr[2], (__bf16)kr[3],
+                                (__bf16)kr[4], (__bf16)kr[5], (__bf16)kr[6], (__bf16)kr[7]};
+        *reinterpret_cast<bf16x8 *>(dst + (int64_t)i * 16) = h;
+    }
+    for (int i = threadIdx.x; i < NP; i += 256) {
+        const int tt = i >> 6;
+        const int g = (i >> 4) & 3;
+        const int d = 16 * tt + (i & 15);
+        const bf16x8 h = bf16x8{(__bf16)Vf[4 * g][d], (__bf16)Vf[4 * g + 1][d], (__bf16)Vf[4 * g + 2][d],
+                                (__bf16)Vf[4 * g + 3][d], (__bf16)Vf[16 + 4 * g][d], (__bf16)Vf[17 + 4 * g][d],
+                                (__bf16)Vf[18 + 4 * g][d], (__bf16)Vf[19 + 4 * g][d]};
+        *reinterpret_cast<bf16x8 *>(dst + 64 * D + (int64_t)i * 16) = h;
+    }
+}
+
+// 16 bytes per lane from sbase + voff into LDS at m0 + 16*lane (m0 restored).
+// Default (cached) loads: each tile image is read by every query block of
+// its unit.
+__device__ __forceinline__ void lds_copy16(const uint8_t *sbase, uint32_t voff, uint32_t m0) {
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "v"(voff), "s"(sbase), "s"(m0)
+        : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Wait until at most n (wave-uniform, 0..16) vector-memory loads are
+// outstanding; larger n waits for all.
+__device__ __forceinline__ void wait_vm_upto(int n) {
+    switch (n) {
+#define GLA_WAIT_CASE(k) \
+    case k:              \
+        wait_vm<k>();    \
+        break;
+        GLA_WAIT_CASE(1) GLA_WAIT_CASE(2) GLA_WAIT_CASE(3) GLA_WAIT_CASE(4) GLA_WAIT_CASE(5) GLA_WAIT_CASE(6)
+        GLA_WAIT_CASE(7) GLA_WAIT_CASE(8) GLA_WAIT_CASE(9) GLA_WAIT_CASE(10) GLA_WAIT_CASE(11) GLA_WAIT_CASE(12)
+        GLA_WAIT_CASE(13) GLA_WAIT_CASE(14) GLA_WAIT_CASE(15) GLA_WAIT_CASE(16)
+#undef GLA_WAIT_CASE
+    default:
+        wait_vm<0>();
+    }
+}
+
+// Waves per workgroup of the staged kernel (32 queries each): as many as the
+// registers allow (d = 64: 4 per SIMD, d = 128: 3, d = 256: 1).
+template <int D>
+constexpr int kBf16sWaves = D == 64 ? 16 : (D == 128 ? 12 : 4);
+
+template <int D>
+__global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(const PrefillParams p,
+                                                                          const uint8_t *img, int n_tiles) {
+    constexpr int NW = kBf16sWaves<D>, NT = 2;
+    constexpr int QW = 16 * NT;
+    constexpr int KS = D / 32;
+    constexpr int DT = D / 16;
+    constexpr int NC = kTileImage<D> / 1024;  // 1 KB copies per tile, dealt to the waves in turn
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kRingTiles][kTileImage<D>];
+
+    const int n_hgrp = p.group / p.hpw;
+    const int unit = blockIdx.x;
+    const int b = unit / (p.n_kv_heads * n_hgrp);
+    const int kvh = (unit - b * p.n_kv_heads * n_hgrp) / n_hgrp;
+    const int hgrp = unit - (b * p.n_kv_heads + kvh) * n_hgrp;
+    const int qblk = p.n_qblocks - 1 - (int)blockIdx.y;
+    const int waves_per_head = NW / p.hpw;
+    const int qwg = QW * waves_per_head;
+
+    const int row0 = p.q_start[b];
+    const int q_len = min(max(p.q_start[b + 1] - row0, 0), p.max_q_len);
+    const int pos0 = p.pos_offset[b];
+    const int qb0 = qblk * qwg;
+    if (qb0 >= q_len) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 15;
+    const int lgrp = lane >> 4;
+    const int head = kvh * p.group + hgrp * p.hpw + (wave % p.hpw);
+    const int wq0 = qb0 + (wave / p.hpw) * QW;
+
+    const int q_last = min(q_len, qb0 + qwg) - 1;
+    const int khi = min(pos0 + q_last, p.pm.pos_limit - 1);
+    const int klo = window_lo(pos0 + qb0, p.sliding_window);
+
+    bf16x8 qb[NT][KS];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int lq = wq0 + nt * 16 + lrow;
+        const bool ok = lq < q_len;
+        const float *qp = p.q + ((int64_t)(row0 + (ok ? lq : 0)) * p.n_heads + head) * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const float4 a = *reinterpret_cast<const float4 *>(qp + ks * 32 + lgrp * 8);
+            const float4 c = *reinterpret_cast<const float4 *>(qp + ks * 32 + lgrp * 8 + 4);
+            const float mul = ok ? p.q_mul : 0.0f;
+            qb[nt][ks] = bf16x8{(__bf16)(a.x * mul), (__bf16)(a.y * mul), (__bf16)(a.z * mul), (__bf16)(a.w * mul),
+                                (__bf16)(c.x * mul), (__bf16)(c.y * mul), (__bf16)(c.z * mul), (__bf16)(c.w * mul)};
+        }
+    }
+
+    floatx4 o[DT][NT];
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) o[t][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[NT], lpart[NT];
+    int qpos[NT], qlo[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        m[nt] = -INFINITY;
+        lpart[nt] = 0.0f;
+        const int lq = wq0 + nt * 16 + lrow;
+        qpos[nt] = lq < q_len ? pos0 + lq : -1;
+        qlo[nt] = window_lo(pos0 + lq, p.sliding_window);
+    }
+
+    if (khi >= klo) {
+        const int tfirst = klo / KT;
+        const int n = khi / KT - tfirst + 1;
+        const uint8_t *unit_img = img + ((int64_t)b * p.n_kv_heads + kvh) * n_tiles * kTileImage<D>;
+        const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(
+            (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)&ring[0][0]);
+        // this wave's share of a tile: kilobytes wave, wave + NW, ... (below NC)
+        const int my_copies = wave < NC ? (NC - wave + NW - 1) / NW : 0;
+        auto issue = [&](int i) {
+            const uint8_t *src = unit_img + (int64_t)(tfirst + i) * kTileImage<D>;
+            const uint32_t dst = ring_lds + (uint32_t)((i % kRingTiles) * kTileImage<D>);
+#pragma unroll
+            for (int c = wave; c < NC; c += NW)
+                lds_copy16(src, (uint32_t)(c * 1024 + lane * 16), dst + c * 1024);
+        };
+#pragma unroll
+        for (int i = 0; i < kRingTiles - 1; i++)
+            if (i < n) issue(i);
+        for (int i = 0; i < n; i++) {
+            // this wave's copies of tile i have landed (later tiles may be in flight) ...
+            wait_vm_upto(min(kRingTiles - 2, n - 1 - i) * my_copies);
+            // ... and every wave's have; every wave is also done with tile i - 1,
+            // whose buffer the next copy reuses
+            __syncthreads();
+            if (i + kRingTiles - 1 < n) issue(i + kRingTiles - 1);
+            const int k0 = (tfirst + i) * KT;
+            const uint8_t *kimg = ring[i % kRingTiles];
+            const uint8_t *vimg = kimg + 64 * D;
+
+            // S^T = K . Q^T
+            floatx4 sacc[2][NT];
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) sacc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                bf16x8 a[2];
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+                    a[mt] = *reinterpret_cast<const bf16x8 *>(kimg + ((mt * (D / 8) + ks * 4 + lgrp) * 16 + lrow) * 16);
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++)
+                        sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt], qb[nt][ks], sacc[mt][nt], 0, 0, 0);
+            }
+
+            const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
+                                  (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
+            bf16x8 pb[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+                    for (int i2 = 0; i2 < 4; i2++) {
+                        const int kp = k0 + mt * 16 + 4 * lgrp + i2;
+                        float x = sacc[mt][nt][i2];
+                        if (p.softcap > 0.0f) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
+                        if (!interior) {
+                            const bool ok = kp <= qpos[nt] && kp >= qlo[nt] && kp >= klo && kp <= khi;
+                            x = ok ? x : -INFINITY;
+                        }
+                        sacc[mt][nt][i2] = x;
+                        mx = fmaxf(mx, x);
+                    }
+                }
+                mx = max_rows4(mx);
+                const float m_new = fmaxf(m[nt], mx);
+                if (m_new == -INFINITY) {
+                    pb[nt] = bf16x8{};
+                    continue;
+                }
+                const float rs = fast_exp2(m[nt] - m_new);
+                m[nt] = m_new;
+                float pr[2][4];
+                float ls = 0.0f;
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                    for (int i2 = 0; i2 < 4; i2++) {
+                        // the sum uses the bf16 value the MFMA multiplies
+                        const __bf16 h = (__bf16)fast_exp2(sacc[mt][nt][i2] - m_new);
+                        pr[mt][i2] = (float)h;
+                        ls += pr[mt][i2];
+                    }
+                pb[nt] = bf16x8{(__bf16)pr[0][0], (__bf16)pr[0][1], (__bf16)pr[0][2], (__bf16)pr[0][3],
+                                (__bf16)pr[1][0], (__bf16)pr[1][1], (__bf16)pr[1][2], (__bf16)pr[1][3]};
+                lpart[nt] = lpart[nt] * rs + ls;
+                if (__ballot(rs != 1.0f)) {
+#pragma unroll
+                    for (int t = 0; t < DT; t++) o[t][nt] *= rs;
+                }
+            }
+
+            // O^T += V^T . P^T
+#pragma unroll
+            for (int t = 0; t < DT; t++) {
+                const bf16x8 a = *reinterpret_cast<const bf16x8 *>(vimg + ((t * 4 + lgrp) * 16 + lrow) * 16);
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    o[t][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[nt], o[t][nt], 0, 0, 0);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        float lt = lpart[nt];
+        lt = sum_rows4(lt);
+        const int lq = wq0 + nt * 16 + lrow;
+        if (lq >= q_len) continue;
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        float *op = p.out + ((int64_t)(row0 + lq) * p.n_heads + head) * D;
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            const floatx4 v = o[t][nt] * inv;
+            *reinterpret_cast<float4 *>(op + 16 * t + 4 * lgrp) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+}
+
+// The staged path's launches; GLA_ERR_* when a launch fails.
+template <int D, bool Q8>
+int launch_bf16_staged(gla_ctx *ctx, const PrefillParams &prm, dim3 grid, int n_seqs, uint8_t *img, int n_tiles) {
+    hipLaunchKernelGGL((stage_bf16_kernel<D, Q8>), dim3(n_tiles, prm.n_kv_heads, n_seqs), dim3(256), 0, ctx->stream,
+                       prm, img, n_tiles);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "stage_bf16_kernel launch: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL((prefill_bf16s_kernel<D>), grid, dim3(kBf16sWaves<D> * 64), 0, ctx->stream, prm,
+                       (const uint8_t *)img, n_tiles);
+    e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "prefill_bf16s_kernel launch: %s", hipGetErrorString(e));
+    return GLA_OK;
+}
+
 template <int D, bool Q8>
 int launch_bf16(gla_ctx *ctx, const PrefillParams &prm, dim3 grid) {
     hipLaunchKernelGGL((prefill_bf16_kernel<D, Q8>), grid, dim3(kBf16Waves<D> * 64), 0, ctx->stream, prm);
@@ -774,8 +1093,20 @@ int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
     default:
         return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
     }
-    if (a.precision == GLA_PREC_BF16)  // prefill_bf16_kernel's shape
-        NT = 2, NW = D == 256 ? kBf16Waves<256> : kBf16Waves<128>;
+    // bf16: the staged path keeps the bf16 tile images of every (sequence, KV
+    // head) in scratch, up to 1 GiB; beyond that each workgroup converts its
+    // own tiles (prefill_bf16_kernel)
+    const int n_tiles = (a.pm.pos_limit + KT - 1) / KT;
+    const size_t img_bytes = (size_t)a.n_seqs * a.n_kv_heads * (size_t)n_tiles * (size_t)(128 * D);
+    const bool staged = a.precision == GLA_PREC_BF16 && getenv("GLA_BF16_UNSTAGED") == nullptr && n_tiles > 0 &&
+                        img_bytes <= ((size_t)1 << 30);
+    if (a.precision == GLA_PREC_BF16) {
+        NT = 2;
+        if (staged)
+            NW = D == 64 ? kBf16sWaves<64> : (D == 128 ? kBf16sWaves<128> : kBf16sWaves<256>);
+        else
+            NW = D == 256 ? kBf16Waves<256> : kBf16Waves<128>;
+    }
     const int qwg = 16 * NT * (NW / hpw);
     PrefillParams prm;
     prm.kv = a.kv;
@@ -797,6 +1128,22 @@ int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
     if (prm.n_qblocks > 65535) return set_error(GLA_ERR_INVALID, "prefill: %d query blocks > 65535", prm.n_qblocks);
     dim3 grid(a.n_seqs * a.n_kv_heads * (group / hpw), prm.n_qblocks, 1);
     if (a.precision == GLA_PREC_BF16) {
+        if (staged) {
+            int rc = ensure_scratch(ctx, img_bytes);
+            if (rc != GLA_OK) return rc;
+            uint8_t *img = (uint8_t *)ctx->scratch;
+            switch (D) {
+            case 64:
+                return a.q8 ? launch_bf16_staged<64, true>(ctx, prm, grid, a.n_seqs, img, n_tiles)
+                            : launch_bf16_staged<64, false>(ctx, prm, grid, a.n_seqs, img, n_tiles);
+            case 128:
+                return a.q8 ? launch_bf16_staged<128, true>(ctx, prm, grid, a.n_seqs, img, n_tiles)
+                            : launch_bf16_staged<128, false>(ctx, prm, grid, a.n_seqs, img, n_tiles);
+            default:
+                return a.q8 ? launch_bf16_staged<256, true>(ctx, prm, grid, a.n_seqs, img, n_tiles)
+                            : launch_bf16_staged<256, false>(ctx, prm, grid, a.n_seqs, img, n_tiles);
+            }
+        }
         switch (D) {
         case 64:
             return a.q8 ? launch_bf16<64, true>(ctx, prm, grid) : launch_bf16<64, false>(ctx, prm, grid);

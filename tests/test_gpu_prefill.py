@@ -41,7 +41,10 @@ def test_prefill_varlen_batch(backend, dtype, d, H, Hkv):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "q8"])
-def test_prefill_paged(backend, dtype):
+@pytest.mark.parametrize("precision", ["f32", "bf16"])
+def test_prefill_paged(backend, dtype, precision):
+    """Paged pools; the table is 17 pages wide (272 positions, not a multiple of the 32-key
+    tile), and the last sequence's last tile runs past it."""
     H, Hkv, d = 8, 2, 128
     ctx = np.array([100, 37, 260], np.int32)
     pb = synth.paged_batch(41, ctx, prefix_tokens=32)
@@ -51,12 +54,34 @@ def test_prefill_paged(backend, dtype):
     offs = ctx - n
     q = synth.normal(43, (int(n.sum()), H, d))
     q_start = np.concatenate([[0], np.cumsum(n)]).astype(np.int32)
+    tol = (BF16_ABS_TOL, BF16_REL_TOL) if precision == "bf16" else ()
     for window in (None, 40):
-        got = run_prefill(backend, p.pool, q, q_start, offs, H, 0.09, None, window, table=pb.table)
+        got = run_prefill(backend, p.pool, q, q_start, offs, H, 0.09, None, window, table=pb.table,
+                          precision=precision)
         for b in range(3):
             rows = slice(q_start[b], q_start[b + 1])
             want = _oracle_prefill(p.stores[b], q[rows], int(offs[b]), H, Hkv, d, 0.09, None, window)
-            assert_close(got[rows], want, what=f"paged {dtype} seq {b} window {window}")
+            assert_close(got[rows], want, *tol, what=f"paged {dtype} {precision} seq {b} window {window}")
+
+
+@pytest.mark.parametrize("d,H,Hkv", [(128, 8, 2), (64, 9, 3), (256, 4, 2)])
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+def test_prefill_bf16_staged_equals_unstaged(backend, monkeypatch, dtype, d, H, Hkv):
+    """The bf16 path with the tile images staged once per call (the default) and with each
+    workgroup converting its own tiles (GLA_BF16_UNSTAGED) round the same values and feed the
+    MFMAs in the same order: bit-identical outputs, windows and soft-cap included."""
+    lens = [70, 1, 130]
+    offs = [0, 40, 17]
+    max_seq = max(o + n for o, n in zip(offs, lens))
+    c = Contig(backend, dtype, 3, 1, max_seq, Hkv, d, seed=870 + d + H)
+    q = synth.normal(970 + d, (sum(lens), H, d))
+    q_start = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    for cap, window in [(None, None), (20.0, 33)]:
+        monkeypatch.delenv("GLA_BF16_UNSTAGED", raising=False)
+        staged = run_prefill(backend, c.cache, q, q_start, offs, H, 0.1, cap, window, precision="bf16")
+        monkeypatch.setenv("GLA_BF16_UNSTAGED", "1")
+        unstaged = run_prefill(backend, c.cache, q, q_start, offs, H, 0.1, cap, window, precision="bf16")
+        assert np.array_equal(staged.view(np.uint32), unstaged.view(np.uint32)), (dtype, d, cap, window)
 
 
 @pytest.mark.parametrize("d,H,Hkv", [(128, 8, 2), (64, 9, 3), (256, 4, 2), (128, 4, 4)])
