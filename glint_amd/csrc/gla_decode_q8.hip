@@ -744,7 +744,10 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
     // sequence's last, short workgroup finish together instead of one wave
     // working while the others wait at the merge.
     const int span = kWaves * p.ch;
-    const int n_wg = (r.n_pages + span - 1) / span;
+    // (at most max_wg: partial slots are sized from the host lengths, and a
+    // caller whose host copies disagree with the device arrays gets a wrong
+    // result, never an access outside the slots)
+    const int n_wg = min((r.n_pages + span - 1) / span, p.max_wg);
     if (wg >= n_wg) return;
     const int wg_pages = min(span, r.n_pages - wg * span);
     const int per_wave = ((wg_pages + 2 * kWaves - 1) / (2 * kWaves)) * 2;  // even: a step is two pages
@@ -810,7 +813,7 @@ __global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p
     const int h_base = kvh * p.group + g0;
     const Range r = seq_range(p, b);
     const int span = kWaves * p.ch;  // pages per workgroup
-    const int n_wg = (r.n_pages + span - 1) / span;
+    const int n_wg = min((r.n_pages + span - 1) / span, p.max_wg);
     if (n_wg <= 1) return;
     const int idx = blockIdx.x * 256 + threadIdx.x;
     const int g = idx / D;

@@ -135,6 +135,31 @@ def test_q8_context_beyond_64_chunks(backend, monkeypatch, host_lengths):
     assert_close(got, want, what="q8 70k context")
 
 
+def test_q8_host_lengths_shorter_than_device(backend, monkeypatch):
+    """Host copies of the lengths that understate the device arrays break the gla_decode_args
+    contract: the launch is sized from them, so the result is not the attention over the device
+    windows, but every partial stays inside the slots sized for the launch (finite output, no
+    error); with matching copies the same call is exact."""
+    monkeypatch.setenv("GLA_Q8_CHUNK_PAGES", "2")  # many partials per unit
+    H, Hkv, d = 8, 2, 64
+    ctx = np.array([900, 40, 333], np.int32)
+    pb = synth.paged_batch(831, ctx)
+    p = Pool(backend, "q8", pb, Hkv, d, seed=832)
+    q = synth.normal(833, (len(ctx), H, d))
+    B = len(ctx)
+    dq, dout = backend.buffer(np.ascontiguousarray(q)), backend.empty(q.nbytes)
+    ds, dl = backend.buffer(pb.kv_start), backend.buffer(pb.kv_len)
+    table = backend.buffer(np.ascontiguousarray(pb.table))
+    short = np.minimum(pb.kv_len, 100).astype(np.int32)
+    backend.decode(p.pool, dq, dout, ds, dl, B, int(pb.kv_len.max()), H, 0.125, None, page_table=table,
+                   page_table_stride=pb.table.shape[1], kv_start_host=pb.kv_start, kv_len_host=short)
+    backend.sync()
+    assert np.all(np.isfinite(dout.download(q.shape)))
+    want = _oracle_decode(p.stores, q, pb.kv_start, pb.kv_len, H, Hkv, d, 0.125)
+    got = run_decode(backend, p.pool, q, pb.kv_start, pb.kv_len, H, 0.125, table=pb.table)
+    assert_close(got, want, what="matching host lengths")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "q8"])
 @pytest.mark.parametrize("paged", [False, True])
 def test_indexing_is_bit_exact(backend, dtype, paged):
