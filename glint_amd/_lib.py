@@ -123,6 +123,12 @@ SIGNATURES = {
     "gla_prefill": (_I, [_P, C.POINTER(PrefillArgs)]),
     "gla_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _P]),
     "gla_attention_resident": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
+    "gla_rope": (_I, [_P, _P, _I, _I, _I, _P, _F, _F, _I]),
+    "gla_q8w_create": (_I, [_P, _P, _I, _I, C.POINTER(_P)]),
+    "gla_q8w_destroy": (_I, [_P]),
+    "gla_q8w_rows": (_I, [_P]),
+    "gla_q8w_cols": (_I, [_P]),
+    "gla_matvec_q8_0": (_I, [_P, _P, _P, _I, _P]),
 }
 
 _lib = None

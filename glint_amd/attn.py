@@ -204,6 +204,24 @@ class DevicePagePool(_KvBase):
         check(_lib.lib().gla_pool_zero_page(self.backend.ctx, self.handle, page))
 
 
+class Q8Weights:
+    """GGML Q8_0 weights uploaded once and repacked for the MFMA matvec (gla_q8w_create)."""
+
+    def __init__(self, backend: "GpuBackend", handle: C.c_void_p, rows: int, cols: int):
+        self.backend, self.handle, self.rows, self.cols = backend, handle, rows, cols
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(_lib.lib().gla_q8w_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
 class GpuBackend:
     """One HIP device and stream (gla_ctx). Mirrors GpuBackend::new's failure mode:
     no device -> GlaError named GpuAdapterNotFound, and the caller keeps its CPU path."""
@@ -339,3 +357,21 @@ class GpuBackend:
         a.q = q.ptr
         a.out = out.ptr
         check(_lib.lib().gla_prefill(self.ctx, C.byref(a)))
+
+    def rope(self, x: DeviceBuffer, n_rows: int, n_heads: int, head_dim: int, pos: DeviceBuffer, freq_base: float,
+             scaling_factor: float = 1.0, rot_dim: Optional[int] = None) -> None:
+        """ops::rope (src/tensor/ops.rs:212-245) in place on device rows x [n_rows][n_heads][head_dim]."""
+        check(_lib.lib().gla_rope(self.ctx, x.ptr, n_rows, n_heads, head_dim, pos.ptr, float(freq_base),
+                                  float(scaling_factor), head_dim if rot_dim is None else rot_dim))
+
+    def create_q8_weights(self, ggml: np.ndarray, rows: int, cols: int) -> Q8Weights:
+        """Upload GGML Q8_0 bytes [rows][cols/32 x 34] (gla_q8w_create)."""
+        raw = np.ascontiguousarray(ggml, dtype=np.uint8).reshape(-1)
+        assert raw.size == rows * (cols // 32) * 34
+        h = C.c_void_p()
+        check(_lib.lib().gla_q8w_create(self.ctx, _ptr(raw), rows, cols, C.byref(h)))
+        return Q8Weights(self, h, rows, cols)
+
+    def matvec_q8_0(self, w: Q8Weights, x: DeviceBuffer, n_vec: int, y: DeviceBuffer) -> None:
+        """y[v] = W x[v] for n_vec device vectors (QuantizedTensor::matvec, src/tensor/quantized.rs:247-346)."""
+        check(_lib.lib().gla_matvec_q8_0(self.ctx, w.handle, x.ptr, n_vec, y.ptr))

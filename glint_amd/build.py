@@ -47,7 +47,8 @@ HIP_FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{ROOT / 'include'}",
 ]
-HIP_SOURCES = ["gla_capi.hip", "gla_kvstore.hip", "gla_decode.hip", "gla_decode_q8.hip", "gla_prefill.hip"]
+HIP_SOURCES = ["gla_capi.hip", "gla_kvstore.hip", "gla_decode.hip", "gla_decode_q8.hip", "gla_prefill.hip",
+               "gla_ops.hip"]
 
 
 def _run(cmd: list[str], cwd: Path | None = None) -> None:

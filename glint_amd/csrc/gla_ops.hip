@@ -1,0 +1,407 @@
+// gla_ops.hip -- the GPU ops beside attention on a decode step: RoPE on q/k
+// and the Q8_0 weight matvec of the Q/K/V/O projections, so the step stays
+// on the device between the projections and attention.
+//
+//   gla_rope          ops::rope                         src/tensor/ops.rs:212-245
+//   gla_q8w_create    GpuBackend::upload_buffer of GGML Q8_0 weights
+//                                                       src/backend/gpu.rs:111-121
+//   gla_matvec_q8_0   QuantizedTensor::matvec / matvec_batch over Q8_0,
+//                     matvec_q8_0.wgsl               src/tensor/quantized.rs:247-346, :587-610
+//
+// Matvec design. GGML's 34-byte blocks ([f16 scale][32 x i8]) are not 16-byte
+// aligned, so the weights are repacked once, on upload, into the operand
+// order of v_mfma_f32_16x16x32_f16: a row tile of 16 rows and a pair of
+// 32-element blocks is one 16-byte piece per lane (lane l: row l%16, elements
+// (l/16)*8 .. +8 of each block, stored as x + 128 so that one v_perm makes
+// the exact f16 of 1024 + byte), and the pair's 32 scales are one 16-byte
+// read per lane. The activations are split per call into two f16 pieces
+// (hi = f16(x * 2^s), lo = f16(x * 2^s - hi), s per vector putting the
+// largest |x| near 2^14), so each block's product runs as two MFMAs with
+// exact int8 x f16 products and f32 accumulation; the f16 block scale is
+// applied in f32 per block, as the reference applies it. A wave owns two row
+// tiles for every vector of the launch (up to 64), so the weights are read
+// once per launch; the workgroup's four waves split the blocks and are merged
+// in LDS. Bound: HBM on the weights (34 bytes per 32 weights).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "gla_internal.h"
+
+struct gla_q8w {
+    gla_ctx *ctx = nullptr;
+    int rows = 0;
+    int cols = 0;
+    int n_tiles = 0;  // ceil(rows / 16)
+    int n_pairs = 0;  // ceil(cols / 64)
+    uint8_t *quants = nullptr;  // [n_tiles][n_pairs][64 lanes][16 B]
+    uint16_t *scales = nullptr;  // [n_tiles][n_pairs][16 rows][2 blocks] f16
+};
+
+namespace gla {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- RoPE -----------------------------------------------------------------
+
+// One thread per (row, head, pair): the pair (i, i+1), i even and below
+// rot = min(rot_dim, head_dim) & ~1, rotated by (pos / scaling) * base^(-i/d),
+// with the reference's f32 operations in its order and no contraction.
+__global__ __launch_bounds__(256) void rope_kernel(float *x, int n_rows, int n_heads, int head_dim, int n_pairs,
+                                                   const int32_t *pos, float freq_base, float scaling_factor) {
+#pragma clang fp contract(off)
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = (int64_t)n_rows * n_heads * n_pairs;
+    if (t >= total) return;
+    const int pr = (int)(t % n_pairs);
+    const int64_t rh = t / n_pairs;
+    const int row = (int)(rh / n_heads);
+    const int i = 2 * pr;
+    const float pos_scaled = (float)pos[row] / scaling_factor;
+    // base^(i/d) correctly rounded to f32 (through double precision), which
+    // is what glibc's powf returns for these arguments, then the reference's
+    // f32 reciprocal: the angles, and so the rotations, match it bit for bit
+    // up to cos/sin's last-place differences
+    const float pw = (float)pow((double)freq_base, (double)((float)i / (float)head_dim));
+    const float freq = 1.0f / pw;
+    const float angle = pos_scaled * freq;
+    const float c = cosf(angle);
+    const float s = sinf(angle);
+    float *p = x + rh * head_dim + i;
+    const float x0 = p[0], x1 = p[1];
+    p[0] = x0 * c - x1 * s;
+    p[1] = x0 * s + x1 * c;
+}
+
+// ---- Q8_0 weights: repack ----------------------------------------------------
+
+// One thread per (row tile, block pair, lane): the lane's 16 quant bytes and,
+// for lanes 0..15, the two scales of row (tile*16 + lane) in the pair.
+__global__ __launch_bounds__(256) void q8w_repack_kernel(const uint8_t *ggml, int rows, int n_blocks, int n_pairs,
+                                                         int64_t n_units, uint8_t *quants, uint16_t *scales) {
+    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (u >= n_units) return;
+    const int lane = (int)(u & 63);
+    const int64_t tp = u >> 6;  // tile * n_pairs + pair
+    const int pair = (int)(tp % n_pairs);
+    const int tile = (int)(tp / n_pairs);
+    const int row = tile * 16 + (lane & 15);
+    const int kg = lane >> 4;
+    uint8_t out[16];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int blk = 2 * pair + j;
+        const bool ok = row < rows && blk < n_blocks;
+        const uint8_t *src = ggml + ((int64_t)row * n_blocks + blk) * 34 + 2 + kg * 8;
+#pragma unroll
+        for (int e = 0; e < 8; e++) out[j * 8 + e] = ok ? (uint8_t)(src[e] ^ 0x80) : (uint8_t)0x80;
+    }
+    uint4 w;
+    w.x = out[0] | (out[1] << 8) | (out[2] << 16) | ((uint32_t)out[3] << 24);
+    w.y = out[4] | (out[5] << 8) | (out[6] << 16) | ((uint32_t)out[7] << 24);
+    w.z = out[8] | (out[9] << 8) | (out[10] << 16) | ((uint32_t)out[11] << 24);
+    w.w = out[12] | (out[13] << 8) | (out[14] << 16) | ((uint32_t)out[15] << 24);
+    *reinterpret_cast<uint4 *>(quants + u * 16) = w;
+    if (lane < 16) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int blk = 2 * pair + j;
+            uint16_t sc = 0;
+            if (row < rows && blk < n_blocks) {
+                const uint8_t *src = ggml + ((int64_t)row * n_blocks + blk) * 34;
+                sc = (uint16_t)(src[0] | (src[1] << 8));
+            }
+            scales[(tp * 16 + lane) * 2 + j] = sc;
+        }
+    }
+}
+
+// ---- activations: f16 pieces ---------------------------------------------------
+
+// One workgroup per vector (vectors past n_vec, up to the padded count, get
+// zero pieces): xp[v][blk][kg] = {hi[8], lo[8]} for the 8 elements
+// blk*32 + kg*8 .. +8, and xs[v] = 2^-s, the factor that undoes the scaling.
+__global__ __launch_bounds__(256) void split_x_kernel(const float *x, int n_vec, int cols, int n_blocks_pad,
+                                                      _Float16 *xp, float *xs) {
+    const int v = blockIdx.x;
+    __shared__ float red[256];
+    float mx = 0.0f;
+    if (v < n_vec)
+        for (int c = threadIdx.x; c < cols; c += 256) mx = fmaxf(mx, fabsf(x[(int64_t)v * cols + c]));
+    red[threadIdx.x] = mx;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    mx = red[0];
+    int e = 0;
+    if (mx > 0.0f && isfinite(mx)) frexpf(mx, &e);  // mx in [2^(e-1), 2^e)
+    const int sh = 14 - e;                             // the largest |x| * 2^sh lies in [2^13, 2^14)
+    const float mul = ldexpf(1.0f, sh);
+    if (threadIdx.x == 0) xs[v] = ldexpf(1.0f, -sh);
+    const int n_units = n_blocks_pad * 4;  // (block, kg) units of 8 elements
+    for (int u = threadIdx.x; u < n_units; u += 256) {
+        const int c0 = u * 8;
+        half8 hi, lo;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float t = (v < n_vec && c0 + k < cols) ? x[(int64_t)v * cols + c0 + k] * mul : 0.0f;
+            const _Float16 h = (_Float16)t;
+            hi[k] = h;
+            lo[k] = (_Float16)(t - (float)h);
+        }
+        _Float16 *dst = xp + ((int64_t)v * n_blocks_pad * 4 + u) * 16;
+        *reinterpret_cast<half8 *>(dst) = hi;
+        *reinterpret_cast<half8 *>(dst + 8) = lo;
+    }
+}
+
+// ---- the matvec ----------------------------------------------------------------------
+
+// 4 bytes x + 128 -> 4 exact f16 (1024 + byte - 1152) at o[at .. at+3].
+__device__ __forceinline__ void bytes_to_h(uint32_t u, half8 &o, int at) {
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x07010700u);  // bytes 0, 1 under 0x64
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x07030702u);  // bytes 2, 3
+    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+    const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const half2v a = __builtin_bit_cast(half2v, lo) - bias;
+    const half2v b = __builtin_bit_cast(half2v, hi) - bias;
+    o[at] = a[0];
+    o[at + 1] = a[1];
+    o[at + 2] = b[0];
+    o[at + 3] = b[1];
+}
+
+constexpr int kRT = 2;  // row tiles per wave
+constexpr int kMaxVT = 4;  // vector tiles (16 vectors each) per launch
+
+template <int NVT>
+__global__ __launch_bounds__(256) void matvec_q8_kernel(const uint8_t *quants, const uint16_t *scales, int rows,
+                                                        int n_tiles, int n_pairs, const _Float16 *xp,
+                                                        const float *xs, int n_blocks_pad, int v0, int n_vec,
+                                                        float *y) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tile0 = blockIdx.x * kRT;
+    const int kg = lane >> 4;
+    const int lc = lane & 15;
+    // this wave's block pairs: an even quarter of them
+    const int per = (n_pairs + 3) / 4;
+    const int p0 = wave * per;
+    const int p1 = min(n_pairs, p0 + per);
+
+    floatx4 acc[kRT][NVT];
+#pragma unroll
+    for (int rt = 0; rt < kRT; rt++)
+#pragma unroll
+        for (int vt = 0; vt < NVT; vt++) acc[rt][vt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int p = p0; p < p1; p++) {
+        uint4 qw[kRT], sw[kRT];
+#pragma unroll
+        for (int rt = 0; rt < kRT; rt++) {
+            const int tile = min(tile0 + rt, n_tiles - 1);
+            const int64_t tp = (int64_t)tile * n_pairs + p;
+            const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(quants + (tp * 64 + lane) * 16));
+            qw[rt] = make_uint4(q.x, q.y, q.z, q.w);
+            sw[rt] = *reinterpret_cast<const uint4 *>(scales + (tp * 16 + kg * 4) * 2);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int blk = 2 * p + j;
+            half8 bh[NVT], bl[NVT];
+#pragma unroll
+            for (int vt = 0; vt < NVT; vt++) {
+                const _Float16 *src = xp + ((int64_t)(v0 + vt * 16 + lc) * n_blocks_pad * 4 + blk * 4 + kg) * 16;
+                bh[vt] = *reinterpret_cast<const half8 *>(src);
+                bl[vt] = *reinterpret_cast<const half8 *>(src + 8);
+            }
+#pragma unroll
+            for (int rt = 0; rt < kRT; rt++) {
+                half8 a;
+                bytes_to_h(j ? qw[rt].z : qw[rt].x, a, 0);
+                bytes_to_h(j ? qw[rt].w : qw[rt].y, a, 4);
+                // scales of rows kg*4 + r: the lane's 16 bytes hold [row][block] f16
+                const uint32_t s01 = j == 0 ? (sw[rt].x & 0xffffu) | (sw[rt].y << 16) : (sw[rt].x >> 16) | (sw[rt].y & 0xffff0000u);
+                const uint32_t s23 = j == 0 ? (sw[rt].z & 0xffffu) | (sw[rt].w << 16) : (sw[rt].z >> 16) | (sw[rt].w & 0xffff0000u);
+                typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+                const half2v h01 = __builtin_bit_cast(half2v, s01);
+                const half2v h23 = __builtin_bit_cast(half2v, s23);
+                const float sc[4] = {(float)h01[0], (float)h01[1], (float)h23[0], (float)h23[1]};
+#pragma unroll
+                for (int vt = 0; vt < NVT; vt++) {
+                    floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh[vt], floatx4{0.0f, 0.0f, 0.0f, 0.0f},
+                                                                      0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl[vt], c, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[rt][vt][r] = fmaf(c[r], sc[r], acc[rt][vt][r]);
+                }
+            }
+        }
+    }
+
+    // merge the four waves' block ranges
+    __shared__ floatx4 red[4][kRT * NVT][64];
+#pragma unroll
+    for (int rt = 0; rt < kRT; rt++)
+#pragma unroll
+        for (int vt = 0; vt < NVT; vt++) red[wave][rt * NVT + vt][lane] = acc[rt][vt];
+    __syncthreads();
+    for (int i = threadIdx.x; i < kRT * NVT * 64; i += 256) {
+        const int rv = i >> 6;
+        const int ln = i & 63;
+        const int rt = rv / NVT;
+        const int vt = rv - rt * NVT;
+        floatx4 s = red[0][rv][ln];
+#pragma unroll
+        for (int w = 1; w < 4; w++) s += red[w][rv][ln];
+        const int tile = tile0 + rt;
+        const int v = v0 + vt * 16 + (ln & 15);
+        if (tile >= n_tiles || v >= n_vec) continue;
+        const float f = xs[v];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = tile * 16 + (ln >> 4) * 4 + r;
+            if (row < rows) y[(int64_t)v * rows + row] = s[r] * f;
+        }
+    }
+}
+
+template <int NVT>
+int launch_matvec(gla_ctx *ctx, const gla_q8w *w, const _Float16 *xp, const float *xs, int n_blocks_pad, int v0,
+                  int n_vec, float *y) {
+    const dim3 grid((w->n_tiles + kRT - 1) / kRT);
+    hipLaunchKernelGGL((matvec_q8_kernel<NVT>), grid, dim3(256), 0, ctx->stream, w->quants, w->scales, w->rows,
+                       w->n_tiles, w->n_pairs, xp, xs, n_blocks_pad, v0, n_vec, y);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "matvec_q8_kernel launch: %s", hipGetErrorString(e));
+    return GLA_OK;
+}
+
+int64_t grid_for(int64_t n) { return (n + 255) / 256; }
+
+}  // namespace
+}  // namespace gla
+
+using namespace gla;
+
+extern "C" {
+
+int gla_rope(gla_ctx *ctx, float *x, int n_rows, int n_heads, int head_dim, const int32_t *pos, float freq_base,
+             float scaling_factor, int rot_dim) {
+    if (!ctx || (!x && n_rows > 0) || (!pos && n_rows > 0)) return set_error(GLA_ERR_INVALID, "gla_rope: NULL argument");
+    if (n_rows < 0 || n_heads <= 0 || head_dim <= 0 || head_dim % 2 || rot_dim < 0)
+        return set_error(GLA_ERR_INVALID, "gla_rope: bad shape (rows %d, heads %d, head_dim %d, rot_dim %d)", n_rows,
+                         n_heads, head_dim, rot_dim);
+    if (!(freq_base > 0.0f) || !(scaling_factor > 0.0f))
+        return set_error(GLA_ERR_INVALID, "gla_rope: freq_base and scaling_factor must be positive");
+    const int rot = std::min(rot_dim, head_dim) & ~1;
+    const int n_pairs = rot / 2;
+    if (n_rows == 0 || n_pairs == 0) return GLA_OK;
+    GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
+    const int64_t total = (int64_t)n_rows * n_heads * n_pairs;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)grid_for(total)), dim3(256), 0, ctx->stream, x, n_rows, n_heads,
+                       head_dim, n_pairs, pos, freq_base, scaling_factor);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "rope_kernel launch: %s", hipGetErrorString(e));
+    return GLA_OK;
+}
+
+int gla_q8w_create(gla_ctx *ctx, const uint8_t *ggml_host, int rows, int cols, gla_q8w **out) {
+    if (!ctx || !ggml_host || !out) return set_error(GLA_ERR_INVALID, "gla_q8w_create: NULL argument");
+    *out = nullptr;
+    if (rows <= 0 || cols <= 0 || cols % 32)
+        return set_error(GLA_ERR_INVALID, "gla_q8w_create: rows %d, cols %d (cols must be a positive multiple of 32)",
+                         rows, cols);
+    GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
+    gla_q8w *w = new gla_q8w();
+    w->ctx = ctx;
+    w->rows = rows;
+    w->cols = cols;
+    w->n_tiles = (rows + 15) / 16;
+    const int n_blocks = cols / 32;
+    w->n_pairs = (n_blocks + 1) / 2;
+    const int64_t n_units = (int64_t)w->n_tiles * w->n_pairs * 64;
+    const size_t raw_bytes = (size_t)rows * n_blocks * 34;
+    uint8_t *raw = nullptr;
+    hipError_t e = hipMalloc(&w->quants, (size_t)n_units * 16);
+    if (e == hipSuccess) e = hipMalloc(&w->scales, (size_t)w->n_tiles * w->n_pairs * 32 * 2);
+    if (e == hipSuccess) e = hipMalloc(&raw, raw_bytes);
+    if (e == hipSuccess) e = hipMemcpyAsync(raw, ggml_host, raw_bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(q8w_repack_kernel, dim3((unsigned)grid_for(n_units)), dim3(256), 0, ctx->stream, raw, rows,
+                           n_blocks, w->n_pairs, n_units, w->quants, w->scales);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (raw) (void)hipFree(raw);
+    if (e != hipSuccess) {
+        (void)hipFree(w->quants);
+        (void)hipFree(w->scales);
+        delete w;
+        return set_error(GLA_ERR_BUFFER, "gla_q8w_create: %s", hipGetErrorString(e));
+    }
+    *out = w;
+    return GLA_OK;
+}
+
+int gla_q8w_destroy(gla_q8w *w) {
+    if (!w) return GLA_OK;
+    if (w->ctx) {
+        (void)hipSetDevice(w->ctx->device);
+        (void)hipStreamSynchronize(w->ctx->stream);
+    }
+    (void)hipFree(w->quants);
+    (void)hipFree(w->scales);
+    delete w;
+    return GLA_OK;
+}
+
+int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, float *y) {
+    if (!ctx || !w || (n_vec > 0 && (!x || !y))) return set_error(GLA_ERR_INVALID, "gla_matvec_q8_0: NULL argument");
+    if (n_vec < 0) return set_error(GLA_ERR_INVALID, "gla_matvec_q8_0: n_vec %d < 0", n_vec);
+    if (n_vec == 0) return GLA_OK;
+    GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
+    const int n_blocks_pad = 2 * w->n_pairs;
+    const int vec_pad = (n_vec + 15) / 16 * 16;
+    const size_t xp_bytes = (size_t)vec_pad * n_blocks_pad * 32 * 2 * sizeof(_Float16);  // hi + lo per element
+    const size_t total = xp_bytes + (size_t)vec_pad * sizeof(float);
+    int rc = ensure_scratch(ctx, total);
+    if (rc != GLA_OK) return rc;
+    _Float16 *xp = (_Float16 *)ctx->scratch;
+    float *xs = (float *)((uint8_t *)ctx->scratch + xp_bytes);
+    hipLaunchKernelGGL(split_x_kernel, dim3(vec_pad), dim3(256), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad, xp,
+                       xs);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "split_x_kernel launch: %s", hipGetErrorString(e));
+    for (int v0 = 0; v0 < n_vec; v0 += 16 * kMaxVT) {
+        const int nvt = std::min(kMaxVT, (n_vec - v0 + 15) / 16);
+        switch (nvt) {
+        case 1:
+            rc = launch_matvec<1>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, y);
+            break;
+        case 2:
+            rc = launch_matvec<2>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, y);
+            break;
+        case 3:
+            rc = launch_matvec<3>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, y);
+            break;
+        default:
+            rc = launch_matvec<4>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, y);
+        }
+        if (rc != GLA_OK) return rc;
+    }
+    return GLA_OK;
+}
+
+int gla_q8w_rows(const gla_q8w *w) { return w ? w->rows : -1; }
+int gla_q8w_cols(const gla_q8w *w) { return w ? w->cols : -1; }
+
+}  // extern "C"

@@ -9,6 +9,8 @@
  *   - PagePool page recycle and copy-on-write       src/cache/paged.rs:79-82, :433-444
  *   - attn_heads_cpu over a batch (decode)          src/transformer/forward.rs:1468-1502
  *   - prefill attention loop                        src/transformer/forward.rs:927-958
+ * and, beside it on a decode step, RoPE (src/tensor/ops.rs:212-245) and the
+ * Q8_0 weight matvec (src/tensor/quantized.rs:247-346, :587-610).
  * The numerics follow flash_attn_1d_ext (src/tensor/flash.rs:46-124).
  *
  * Conventions (the same as Glint's outbound C API, include/glint.h:21-35):
@@ -230,6 +232,34 @@ int gla_attention(gla_ctx *ctx, const float *q, const float *k, const float *v, 
 int gla_attention_resident(gla_ctx *ctx, const float *q, const gla_kv *cache, int seq, int layer,
                            int window_start, int attend_len, int n_heads, float scale, float softcap,
                            float *out);
+
+/* ---- the ops beside attention on a decode step --------------------------- */
+
+/* RoPE in place, ops::rope (src/tensor/ops.rs:212-245) on device rows:
+ * x [n_rows][n_heads][head_dim], row r at position pos[r] (device int32).
+ * For even i < min(rot_dim, head_dim) & ~1 every head's pair (i, i+1) is
+ * rotated by (pos / scaling_factor) * freq_base^(-i / head_dim); the other
+ * dimensions are left as they are. Asynchronous. */
+int gla_rope(gla_ctx *ctx, float *x, int n_rows, int n_heads, int head_dim, const int32_t *pos, float freq_base,
+             float scaling_factor, int rot_dim);
+
+/* Q8_0 weights on the device, uploaded once: the GpuBackend::upload_buffer of
+ * a GGML Q8_0 tensor (src/backend/gpu.rs:111-121), repacked for the MFMA
+ * matvec. ggml_host: rows x (cols / 32) blocks of [f16 scale LE][32 x i8]
+ * (34 bytes); cols a multiple of 32. Returns when the weights are on the
+ * device. */
+typedef struct gla_q8w gla_q8w;
+int gla_q8w_create(gla_ctx *ctx, const uint8_t *ggml_host, int rows, int cols, gla_q8w **out);
+int gla_q8w_destroy(gla_q8w *w);
+int gla_q8w_rows(const gla_q8w *w);
+int gla_q8w_cols(const gla_q8w *w);
+
+/* y[v][r] = sum_c W[r][c] * x[v][c] for n_vec vectors: QuantizedTensor::matvec
+ * and matvec_batch over Q8_0 (src/tensor/quantized.rs:247-346, :587-610; the
+ * wgpu matvec_q8_0 shader's job). x device [n_vec][cols], y device
+ * [n_vec][rows], f32. Asynchronous; the weights are read once per 64
+ * vectors. */
+int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, float *y);
 
 #ifdef __cplusplus
 }

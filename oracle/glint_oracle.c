@@ -16,6 +16,8 @@
  *   src/cache/mod.rs:154-164           KvCache row addressing
  *   src/cache/mod.rs:296-334           KvCacheQ8 quantize_into / dequant_range
  *   src/cache/paged.rs:453-465         PagedKvCache read: table[layer][pos/16], slot pos%16
+ *   src/tensor/ops.rs:212-245          rope (adjacent pairs, partial rot_dim, linear scaling)
+ *   src/tensor/quantized.rs:587-610    matvec_q8_0_scalar (per-block i8 x f32 sums, then x scale)
  *   half 2.7.1 f16::from_f32 / to_f32  (third-party; restated as IEEE round-to-nearest-even)
  *
  * Build flags (oracle/Makefile): -O2 -ffp-contract=off, no fast-math, so the
@@ -475,4 +477,47 @@ static void or_qrows_task(void *p, long r) {
 void or_q8_quantize_rows(const float *src, long n_rows, int n, uint8_t *dst, int n_threads) {
     or_qrows_args a = {src, dst, n, ((n + 31) / 32) * 34};
     or_parallel_for(n_rows, n_threads, or_qrows_task, &a);
+}
+
+/* rope, src/tensor/ops.rs:212-245: x holds whole heads of head_dim; for each
+ * even i < (min(rot_dim, head_dim) & ~1), freq = 1 / base^(i / head_dim),
+ * angle = (pos / scaling_factor) * freq, and every head's pair (i, i+1) is
+ * rotated by angle; the other dimensions are copied. */
+void or_rope(const float *x, float *out, int n, long pos, int head_dim, float freq_base, float scaling_factor,
+             int rot_dim) {
+    memcpy(out, x, (size_t)n * sizeof(float));
+    const float pos_scaled = (float)pos / scaling_factor;
+    const int rot = (rot_dim < head_dim ? rot_dim : head_dim) & ~1;
+    for (int i = 0; i < rot; i += 2) {
+        const float freq = 1.0f / powf(freq_base, (float)i / (float)head_dim);
+        const float angle = pos_scaled * freq;
+        const float c = cosf(angle);
+        const float s = sinf(angle);
+        for (int off = 0; off + head_dim <= n; off += head_dim) {
+            const float x0 = x[off + i];
+            const float x1 = x[off + i + 1];
+            out[off + i] = x0 * c - x1 * s;
+            out[off + i + 1] = x0 * s + x1 * c;
+        }
+    }
+}
+
+/* matvec_q8_0_scalar, src/tensor/quantized.rs:587-610: rows of cols/32
+ * GGML Q8_0 blocks ([f16 scale LE][32 x i8], 34 bytes); out[i] = sum over
+ * blocks of (sum_j i8 * vec[j] in f32, in order) * scale. */
+void or_matvec_q8_0(const uint8_t *data, long rows, int cols, const float *vec, float *out) {
+    const int n_blocks = cols / 32;
+    const size_t bytes_per_row = (size_t)n_blocks * 34;
+    for (long i = 0; i < rows; i++) {
+        const uint8_t *row = data + (size_t)i * bytes_per_row;
+        float sum = 0.0f;
+        for (int b = 0; b < n_blocks; b++) {
+            const uint8_t *block = row + (size_t)b * 34;
+            const float scale = or_f16_to_f32((uint16_t)(block[0] | (block[1] << 8)));
+            float block_sum = 0.0f;
+            for (int j = 0; j < 32; j++) block_sum += (float)(int8_t)block[2 + j] * vec[b * 32 + j];
+            sum += block_sum * scale;
+        }
+        out[i] = sum;
+    }
 }

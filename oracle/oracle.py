@@ -53,6 +53,8 @@ def _bind(path: Path) -> C.CDLL:
     h.or_window_start.argtypes = [_L, _L, _I, _I]
     h.or_decode_batch.argtypes = [_P, _P, _I, _I, _P, _P, _I, _I, _I, _F, _I, _F, _P, _I]
     h.or_prefill.argtypes = [_P, _P, _I, _L, _L, _I, _I, _I, _F, _I, _F, _L, _I, _P, _I]
+    h.or_rope.argtypes = [_P, _P, _I, _L, _I, _F, _F, _I]
+    h.or_matvec_q8_0.argtypes = [_P, _L, _I, _P, _P]
     return h
 
 
@@ -230,4 +232,33 @@ def prefill(q: np.ndarray, store: Store, layer: int, pos_offset: int, n_heads: i
     hc, c = _cap(softcap)
     store.L.or_prefill(_p(q), store.ptr, layer, pos_offset, T, n_heads, n_kv_heads, head_dim, scale, hc, c,
                        int(sliding_window or 0), int(alternating), _p(out), n_threads or threads())
+    return out
+
+
+def rope(x: np.ndarray, pos: int, head_dim: int, freq_base: float, scaling_factor: float, rot_dim: int,
+         L=None) -> np.ndarray:
+    """ops.rs:212-245: rotate the adjacent pairs of every head of x (whole heads of head_dim)."""
+    L = L or lib()
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty_like(x)
+    L.or_rope(_p(x), _p(out), x.size, int(pos), head_dim, freq_base, scaling_factor, rot_dim)
+    return out
+
+
+def q8_0_block(scale: float, quants) -> bytes:
+    """One GGML Q8_0 block: f16 scale (little-endian) then 32 int8 (dequantize.rs test helper layout)."""
+    q = np.asarray(quants, dtype=np.int8)
+    assert q.size == 32
+    return np.array([f16_from_f32(scale)], dtype="<u2").tobytes() + q.tobytes()
+
+
+def matvec_q8_0(data: np.ndarray, rows: int, cols: int, vec: np.ndarray, L=None) -> np.ndarray:
+    """quantized.rs:587-610: GGML Q8_0 rows [rows][cols/32 x 34 B] times vec [cols] -> [rows]."""
+    L = L or lib()
+    data = np.ascontiguousarray(np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray)
+                                else data, dtype=np.uint8)
+    assert data.size == rows * (cols // 32) * 34
+    vec = np.ascontiguousarray(vec, dtype=np.float32)
+    out = np.empty(rows, dtype=np.float32)
+    L.or_matvec_q8_0(_p(data), rows, cols, _p(vec), _p(out))
     return out

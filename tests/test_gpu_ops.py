@@ -1,0 +1,111 @@
+"""The ops beside attention on a decode step, on the GPU through the C ABI: RoPE
+(src/tensor/ops.rs:212-245) and the Q8_0 weight matvec (src/tensor/quantized.rs:247-346,
+:587-610), against the oracle's restatements and an f64 product.
+
+RoPE bar: max abs 1e-5 x max|x| (the angles are computed exactly as the reference computes
+them; cos/sin differ in the last place). Matvec bar: |got - f64| <= 2e-6 x sum_c |w x|, the
+size of f32 rounding over the 4,096-term sums (the fp32 attention bar's 1e-4 absolute does not
+apply to dot products whose terms are O(1000)); the reference's own fixture is matched exactly.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from glint_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _rope_gpu(be, x, pos, head_dim, base, scaling, rot_dim):
+    n_rows, n_heads = x.shape[0], x.shape[1]
+    dx = be.buffer(np.ascontiguousarray(x, np.float32))
+    dp = be.buffer(np.asarray(pos, np.int32))
+    be.rope(dx, n_rows, n_heads, head_dim, dp, base, scaling, rot_dim)
+    be.sync()
+    return dx.download(x.shape)
+
+
+def test_rope_reference_known_answers(backend):
+    """ops.rs tests on the device: position 0 is the identity (full and partial rotary), and
+    pos 2 with scaling 2 equals pos 1 with scaling 1, bit for bit."""
+    x = np.array([[[1.0, 2.0, 3.0, 4.0]]], np.float32)
+    assert np.array_equal(_rope_gpu(backend, x, [0], 4, 10000.0, 1.0, 4), x)
+    assert np.array_equal(_rope_gpu(backend, x, [0], 4, 10000.0, 1.0, 2), x)
+    a = _rope_gpu(backend, x, [2], 4, 10000.0, 2.0, 4)
+    b = _rope_gpu(backend, x, [1], 4, 10000.0, 1.0, 4)
+    assert np.array_equal(a, b)
+    assert np.allclose(a.reshape(-1), orc.rope(x.reshape(-1), 1, 4, 10000.0, 1.0, 4), atol=1e-6)
+
+
+@pytest.mark.parametrize("n_heads,head_dim,rot_dim,base,scaling", [
+    (32, 128, 128, 500000.0, 1.0),   # Llama-3-8B q
+    (8, 128, 128, 500000.0, 1.0),    # its k
+    (9, 64, 64, 10000.0, 1.0),       # SmolLM
+    (4, 96, 48, 10000.0, 4.0),       # Phi-3-style partial rotary, linear scaling
+    (2, 64, 33, 10000.0, 1.0),       # odd rot_dim rounds down
+])
+def test_rope_matches_oracle(backend, n_heads, head_dim, rot_dim, base, scaling):
+    pos = np.array([0, 1, 17, 511, 4095, 8191, 65535], np.int32)
+    x = synth.normal(1200 + head_dim + rot_dim, (len(pos), n_heads, head_dim))
+    got = _rope_gpu(backend, x, pos, head_dim, base, scaling, rot_dim)
+    rot = min(rot_dim, head_dim) & ~1
+    for r, p in enumerate(pos):
+        want = orc.rope(x[r].reshape(-1), int(p), head_dim, base, scaling, rot_dim).reshape(n_heads, head_dim)
+        err = np.abs(got[r] - want).max()
+        assert err <= 1e-5 * np.abs(x[r]).max(), (int(p), err)
+        assert np.array_equal(got[r][:, rot:], x[r][:, rot:])
+
+
+def _q8_rows(rows, cols, seed, mul=1.0):
+    w = synth.normal_rows(seed, rows, cols, mul)
+    return orc.q8_quantize_rows(w).reshape(-1)
+
+
+def _dequant(raw, rows, cols):
+    blk = raw.reshape(rows, cols // 32, 34)
+    scale = blk[:, :, :2].copy().view("<f2").astype(np.float64)
+    q = blk[:, :, 2:].view(np.int8).astype(np.float64)
+    return (q * scale).reshape(rows, cols)
+
+
+def _matvec_gpu(be, raw, rows, cols, x):
+    w = be.create_q8_weights(raw, rows, cols)
+    n_vec = x.shape[0]
+    dx = be.buffer(np.ascontiguousarray(x, np.float32))
+    dy = be.empty(n_vec * rows * 4)
+    be.matvec_q8_0(w, dx, n_vec, dy)
+    be.sync()
+    y = dy.download((n_vec, rows))
+    w.destroy()
+    return y
+
+
+def test_matvec_q8_0_reference_fixture(backend):
+    """quantized.rs test_q8_0_matvec_matches_f32: 10416 and -20832, here exactly (integer
+    products and sums below 2^24, exact in the f16 pieces and the f32 accumulation)."""
+    data = np.frombuffer(orc.q8_0_block(1.0, range(32)) + orc.q8_0_block(2.0, [-i for i in range(32)]), np.uint8)
+    y = _matvec_gpu(backend, data, 2, 32, np.arange(32, dtype=np.float32)[None, :])
+    assert y.tolist() == [[10416.0, -20832.0]]
+
+
+@pytest.mark.parametrize("rows,cols,n_vec", [
+    (6144, 4096, 1),    # Llama-3-8B fused QKV projection, one token
+    (6144, 4096, 64),   # the same over a decode batch of 64
+    (4096, 4096, 5),    # the output projection, a ragged batch
+    (100, 96, 70),      # a row tail (100 = 6 x 16 + 4), an odd block count, two vector launches
+    (16, 32, 17),
+])
+def test_matvec_q8_0_matches_oracle_and_f64(backend, rows, cols, n_vec):
+    raw = _q8_rows(rows, cols, 1300 + rows + n_vec)
+    x = synth.normal(1400 + cols + n_vec, (n_vec, cols))
+    x[0, :7] *= 1e4     # a few large entries: the per-vector piece scale follows the largest
+    got = _matvec_gpu(backend, raw, rows, cols, x)
+    wd = _dequant(raw, rows, cols)
+    exact = x.astype(np.float64) @ wd.T
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wd).T
+    assert np.all(np.abs(got - exact) <= 2e-6 * mag), np.max(np.abs(got - exact) / mag)
+    for v in (0, n_vec // 2, n_vec - 1):
+        want = orc.matvec_q8_0(raw, rows, cols, x[v])
+        assert np.all(np.abs(got[v] - want) <= 4e-6 * mag[v]), v

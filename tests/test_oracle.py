@@ -384,3 +384,90 @@ def test_planted_mistake_is_caught(mutant, tmp_path_factory):
     for check in MUTANT_CHECKS[mutant]:
         with pytest.raises(AssertionError):
             check(L)
+
+
+# ---- RoPE (src/tensor/ops.rs:212-245) and Q8_0 matvec (src/tensor/quantized.rs:587-610) ----
+
+def _rope_f64(x, pos, head_dim, base, scaling, rot_dim):
+    """The rotation in float64: every head's adjacent pair (i, i+1) by (pos/scaling) * base^(-i/d)."""
+    x = np.asarray(x, np.float64).reshape(-1, head_dim).copy()
+    out = x.copy()
+    rot = min(rot_dim, head_dim) & ~1
+    for i in range(0, rot, 2):
+        a = (pos / scaling) * base ** (-i / head_dim)
+        c, s = np.cos(a), np.sin(a)
+        out[:, i] = x[:, i] * c - x[:, i + 1] * s
+        out[:, i + 1] = x[:, i] * s + x[:, i + 1] * c
+    return out.reshape(-1)
+
+
+def test_rope_reference_known_answers():
+    """ops.rs tests: position 0 is the identity (full and partial rotary), and pos 2 with
+    scaling 2 equals pos 1 with scaling 1 bit for bit (both angles are exactly 1.0 x freq)."""
+    x = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    assert np.array_equal(orc.rope(x, 0, 4, 10000.0, 1.0, 4), x)
+    assert np.array_equal(orc.rope(x, 0, 4, 10000.0, 1.0, 2), x)
+    assert np.array_equal(orc.rope(x, 2, 4, 10000.0, 2.0, 4), orc.rope(x, 1, 4, 10000.0, 1.0, 4))
+
+
+@pytest.mark.parametrize("head_dim,rot_dim,scaling", [(64, 64, 1.0), (128, 128, 1.0), (128, 64, 1.0),
+                                                      (128, 65, 1.0), (96, 96, 4.0)])
+def test_rope_vs_f64(head_dim, rot_dim, scaling):
+    """Against the float64 rotation at positions up to 8191 (angles up to ~8,000 rad: the f32
+    angle's own rounding dominates, ~1e-3 rad there, so the bound grows with pos); dimensions
+    past rot_dim (rounded down to even) are copied bit for bit; every rotated pair keeps its
+    length."""
+    rng = np.random.default_rng(head_dim + rot_dim)
+    x = rng.standard_normal(3 * head_dim).astype(np.float32)
+    rot = min(rot_dim, head_dim) & ~1
+    for pos in (0, 1, 17, 511, 4095, 8191):
+        got = orc.rope(x, pos, head_dim, 500000.0, scaling, rot_dim)
+        want = _rope_f64(x, pos, head_dim, 500000.0, scaling, rot_dim)
+        tol = 1e-5 + 4e-7 * pos / scaling
+        assert np.abs(got - want).max() <= tol * np.abs(x).max() * 2, (pos, np.abs(got - want).max())
+        g = got.reshape(-1, head_dim)
+        xx = x.reshape(-1, head_dim)
+        assert np.array_equal(g[:, rot:], xx[:, rot:])
+        n_got = np.hypot(g[:, 0:rot:2], g[:, 1:rot:2])
+        n_x = np.hypot(xx[:, 0:rot:2], xx[:, 1:rot:2])
+        assert np.allclose(n_got, n_x, rtol=1e-6, atol=1e-6)
+
+
+def test_matvec_q8_0_reference_fixture():
+    """quantized.rs test_q8_0_matvec_matches_f32: rows [0..31] x scale 1 and [0..-31] x scale 2
+    against vec [0..31] give sum(i^2) = 10416 and -2 * 10416 (within 0.1, the reference's bar;
+    here exactly, all products and sums being integers below 2^24)."""
+    data = orc.q8_0_block(1.0, range(32)) + orc.q8_0_block(2.0, [-i for i in range(32)])
+    got = orc.matvec_q8_0(np.frombuffer(data, np.uint8), 2, 32, np.arange(32, dtype=np.float32))
+    assert got.tolist() == [10416.0, -20832.0]
+
+
+def test_matvec_q8_0_multi_block_vs_f64():
+    """quantized.rs test_q8_0_simd_matches_scalar's 4 x 128 fixture (quants (r*4+b)*(j+1) as
+    wrapping i8, scale 0.1*(r+1), vec i*0.01) and random 64 x 512 rows, against the float64
+    product of the dequantised rows (scales as stored in f16)."""
+    data = b""
+    for r in range(4):
+        for b in range(4):
+            q = [np.int8(np.uint8(((r * 4 + b) * (j + 1)) & 0xFF).view(np.int8)) for j in range(32)]
+            data += orc.q8_0_block(0.1 * (r + 1), q)
+    vec = (np.arange(128) * 0.01).astype(np.float32)
+    for raw, rows, cols, v in [(np.frombuffer(data, np.uint8), 4, 128, vec), _random_q8(64, 512, 5)]:
+        got = orc.matvec_q8_0(raw, rows, cols, v)
+        want = _q8_dequant_rows(raw, rows, cols) @ v.astype(np.float64)
+        mag = np.abs(_q8_dequant_rows(raw, rows, cols)) @ np.abs(v.astype(np.float64))
+        assert np.all(np.abs(got - want) <= 1e-6 * mag + 1e-6)
+
+
+def _q8_dequant_rows(raw, rows, cols):
+    blk = raw.reshape(rows, cols // 32, 34)
+    scale = blk[:, :, :2].copy().view("<f2").astype(np.float64)
+    q = blk[:, :, 2:].view(np.int8).astype(np.float64)
+    return (q * scale).reshape(rows, cols)
+
+
+def _random_q8(rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((rows, cols)).astype(np.float32)
+    raw = orc.q8_quantize_rows(w).reshape(-1)
+    return raw, rows, cols, rng.standard_normal(cols).astype(np.float32)
