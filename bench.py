@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 attention path on BASELINE.json's configurations.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|cfg1|cfg2|cfg3|cfg4|cfg5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|cfg1|cfg2|cfg3|cfg4|cfg5|proj]
                     [--no-cpu] [--calibrate]
 
 Prints ONE JSON line. `value` is BASELINE's headline metric on its headline
@@ -8,7 +8,8 @@ workload: achieved HBM GB/s of Llama-3-8B-shaped paged Q8_0 decode attention
 at batch 64 (config 3), with every input resident in HBM. The other
 configurations are reported under "secondary": config 1 (SmolLM decode
 latency), config 2 (32 layers of f32 decode), config 4 (4x2048 causal
-prefill, TFLOP/s) and config 5 (Gemma-2 windowed + global decode).
+prefill, TFLOP/s), config 5 (Gemma-2 windowed + global decode) and "proj",
+the Q8_0 QKV projection matvec beside attention (1 and 64 tokens).
 
 A step is one gla_decode (or gla_prefill) call over the whole batch for one
 layer. W untimed steps, then K steps between two HIP events recorded on the
@@ -20,8 +21,8 @@ serve repeats.
 roofline: algorithmic bytes of one call (unique K/V bytes of the attended
 positions, page-table entries, q and out) divided by the call's average
 duration; the call is decode_q8_mfma_kernel + decode_q8_combine_kernel.
-`traffic` comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed
-in profiles/decode_q8_cfg3_pmc.md (calibrated against a page-copy kernel of
+`traffic` comes from the rocprofv3 request-size counter summary committed in
+profiles/decode_q8_cfg3_pmc.md (calibrated against a page-copy kernel of
 known size, see --calibrate), or is null when that file is absent.
 
 cpu_baseline: the C restatement of Glint's CPU flash path (oracle/) on the
@@ -329,6 +330,54 @@ class Prefill:
                            f"per query position, {el:.1f} s")
 
 
+class ProjMatvec:
+    """The Q8_0 weight matvec beside attention (gla_matvec_q8_0): Llama-3-8B's fused QKV projection
+    (6144 x 4096 GGML Q8_0, 26.7 MB) for n_vec tokens, over 16 layers' weights in rotation (427 MB,
+    past the 256 MB last-level cache). Synthetic GGML bytes: int8 quants uniform in [-127, 127], f16
+    scales |N(0, 1)| / 127."""
+
+    def __init__(self, be, n_vec, rows=6144, cols=4096, n_layers=16, seed=0x5151):
+        self.be, self.n_vec, self.rows, self.cols = be, n_vec, rows, cols
+        rng = np.random.default_rng(seed)
+        nb = cols // 32
+        self.w, self.raw0 = [], None
+        for layer in range(n_layers):
+            blk = np.empty((rows, nb, 34), np.uint8)
+            blk[:, :, 2:] = rng.integers(-127, 128, (rows, nb, 32), dtype=np.int8).view(np.uint8)
+            sc = (np.abs(rng.standard_normal((rows, nb))) / 127).astype(np.float16)
+            blk[:, :, :2] = sc.view(np.uint8).reshape(rows, nb, 2)
+            if layer == 0:
+                self.raw0 = blk.reshape(-1).copy()
+            self.w.append(be.create_q8_weights(blk, rows, cols))
+        self.x_host = rng.standard_normal((n_vec, cols)).astype(np.float32)
+        self.x = be.buffer(self.x_host)
+        self.y = be.empty(n_vec * rows * 4)
+        be.sync()
+
+    def step(self, i):
+        self.be.matvec_q8_0(self.w[i % len(self.w)], self.x, self.n_vec, self.y)
+
+    def bytes_per_step(self):
+        return float(self.rows * self.cols // 32 * 34 + self.n_vec * (self.cols + self.rows) * 4)
+
+    def cpu_baseline(self, min_seconds=3.0, max_reps=50):
+        """One layer's QKV matvec for one token through the oracle's restatement of
+        matvec_q8_0_scalar (quantized.rs:587-610), one thread."""
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as orc
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            orc.matvec_q8_0(self.raw0, self.rows, self.cols, self.x_host[0])
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= min_seconds or reps >= max_reps:
+                break
+        nbytes = self.rows * self.cols // 32 * 34 * reps
+        return dict(value=round(nbytes / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                    sample=f"{reps} x one token through layer 0's 6144 x 4096 weights, oracle matvec_q8_0 "
+                           f"(scalar), {el:.1f} s")
+
+
 def calibrate(be: GpuBackend, n_copies: int = 2048) -> dict:
     """Known-size copies for the FETCH_SIZE / WRITE_SIZE scale: gla_pool_copy_page on a
     Q8_0 pool of the cfg3 shape copies one page (34,816 bytes read and written) per dispatch."""
@@ -377,7 +426,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="all", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "all"])
+    ap.add_argument("--workload", default="all", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "proj", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--calibrate", action="store_true", help="also run known-size page copies (for PMC runs)")
     ap.add_argument("--achievable", action="store_true",
@@ -390,7 +439,7 @@ def main() -> int:
 
     be = GpuBackend(0)
     ev = HipEvents()
-    want = {args.workload} if args.workload != "all" else {"cfg1", "cfg2", "cfg3", "cfg4", "cfg5"}
+    want = {args.workload} if args.workload != "all" else {"cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "proj"}
     result = {
         "metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -504,6 +553,25 @@ def main() -> int:
             "tolerance": "max abs 3e-2 / rel 3e-2 vs the fp32 oracle (tests/test_gpu_prefill.py)"}
         log(f"cfg4 bf16: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
         del wl
+    if "proj" in want:
+        for n_vec in (1, 64):
+            log(f"proj: Q8_0 QKV matvec, {n_vec} token(s)")
+            wl = ProjMatvec(be, n_vec)
+            ms = time_steps(be, ev, wl.step, max(args.steps, 50), args.warmup)
+            gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
+            key = f"proj_qkv_b{n_vec}"
+            secondary[key] = {
+                "workload": f"Llama-3-8B fused QKV projection, 6144 x 4096 GGML Q8_0 weights (16 layers in "
+                            f"rotation), {n_vec} token(s) per call (gla_matvec_q8_0)",
+                "value": round(gbs, 2), "unit": "GB/s", "us_per_call": round(ms * 1e3, 2),
+                "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs")}
+            if not args.no_cpu and n_vec == 1:
+                secondary[key]["cpu_baseline"] = wl.cpu_baseline()
+            log(f"{key}: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s")
+            for w in wl.w:
+                w.destroy()
+            del wl
     if args.calibrate:
         log("calibration copies")
         result["calibration"] = calibrate(be)

@@ -18,10 +18,12 @@
 // (hi = f16(x * 2^s), lo = f16(x * 2^s - hi), s per vector putting the
 // largest |x| near 2^14), so each block's product runs as two MFMAs with
 // exact int8 x f16 products and f32 accumulation; the f16 block scale is
-// applied in f32 per block, as the reference applies it. A wave owns two row
-// tiles for every vector of the launch (up to 64), so the weights are read
-// once per launch; the workgroup's four waves split the blocks and are merged
-// in LDS. Bound: HBM on the weights (34 bytes per 32 weights).
+// applied in f32 per block, as the reference applies it. A workgroup owns one
+// row tile (two when there are several vector tiles) for every vector of the
+// launch (up to 64), so the weights are read once per launch; its eight waves
+// split the blocks, each issuing the loads of eight block pairs before
+// computing them, and are merged in LDS. Bound: HBM on the weights (34 bytes
+// per 32 weights).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -124,43 +126,53 @@ __global__ __launch_bounds__(256) void q8w_repack_kernel(const uint8_t *ggml, in
 
 // ---- activations: f16 pieces ---------------------------------------------------
 
-// One workgroup per vector (vectors past n_vec, up to the padded count, get
-// zero pieces): xp[v][blk][kg] = {hi[8], lo[8]} for the 8 elements
-// blk*32 + kg*8 .. +8, and xs[v] = 2^-s, the factor that undoes the scaling.
+// Grid (chunks of 256 units, padded vector count); vectors past n_vec get
+// zero pieces. Each workgroup finds its vector's largest |x| itself (all of
+// the vector's loads in flight at once), then writes the pieces of its chunk:
+// xp[v][blk][kg] = {hi[8], lo[8]} for the 8 elements blk*32 + kg*8 .. +8,
+// and xs[v] = 2^-s, the factor that undoes the scaling.
+constexpr int kSplitUnroll = 8;
 __global__ __launch_bounds__(256) void split_x_kernel(const float *x, int n_vec, int cols, int n_blocks_pad,
                                                       _Float16 *xp, float *xs) {
-    const int v = blockIdx.x;
-    __shared__ float red[256];
+    const int v = blockIdx.y;
+    const float *xv = x + (int64_t)min(v, n_vec - 1) * cols;
     float mx = 0.0f;
-    if (v < n_vec)
-        for (int c = threadIdx.x; c < cols; c += 256) mx = fmaxf(mx, fabsf(x[(int64_t)v * cols + c]));
-    red[threadIdx.x] = mx;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-        __syncthreads();
+    if (v < n_vec) {
+        for (int c0 = 0; c0 < cols; c0 += 256 * kSplitUnroll) {
+            float t[kSplitUnroll];
+#pragma unroll
+            for (int u = 0; u < kSplitUnroll; u++) {
+                const int c = c0 + threadIdx.x + u * 256;
+                t[u] = xv[min(c, cols - 1)];  // clamped: a repeat of the last element
+            }
+#pragma unroll
+            for (int u = 0; u < kSplitUnroll; u++) mx = fmaxf(mx, fabsf(t[u]));
+        }
     }
-    mx = red[0];
+    __shared__ float red[4];
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     int e = 0;
     if (mx > 0.0f && isfinite(mx)) frexpf(mx, &e);  // mx in [2^(e-1), 2^e)
     const int sh = 14 - e;                             // the largest |x| * 2^sh lies in [2^13, 2^14)
     const float mul = ldexpf(1.0f, sh);
-    if (threadIdx.x == 0) xs[v] = ldexpf(1.0f, -sh);
-    const int n_units = n_blocks_pad * 4;  // (block, kg) units of 8 elements
-    for (int u = threadIdx.x; u < n_units; u += 256) {
-        const int c0 = u * 8;
-        half8 hi, lo;
+    if (blockIdx.x == 0 && threadIdx.x == 0) xs[v] = ldexpf(1.0f, -sh);
+    const int u = blockIdx.x * 256 + threadIdx.x;  // (block, kg) unit of 8 elements
+    if (u >= n_blocks_pad * 4) return;
+    const int c0 = u * 8;
+    half8 hi, lo;
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float t = (v < n_vec && c0 + k < cols) ? x[(int64_t)v * cols + c0 + k] * mul : 0.0f;
-            const _Float16 h = (_Float16)t;
-            hi[k] = h;
-            lo[k] = (_Float16)(t - (float)h);
-        }
-        _Float16 *dst = xp + ((int64_t)v * n_blocks_pad * 4 + u) * 16;
-        *reinterpret_cast<half8 *>(dst) = hi;
-        *reinterpret_cast<half8 *>(dst + 8) = lo;
+    for (int k = 0; k < 8; k++) {
+        const float t = (v < n_vec && c0 + k < cols) ? xv[c0 + k] * mul : 0.0f;
+        const _Float16 h = (_Float16)t;
+        hi[k] = h;
+        lo[k] = (_Float16)(t - (float)h);
     }
+    _Float16 *dst = xp + ((int64_t)v * n_blocks_pad * 4 + u) * 16;
+    *reinterpret_cast<half8 *>(dst) = hi;
+    *reinterpret_cast<half8 *>(dst + 8) = lo;
 }
 
 // ---- the matvec ----------------------------------------------------------------------
@@ -179,40 +191,39 @@ __device__ __forceinline__ void bytes_to_h(uint32_t u, half8 &o, int at) {
     o[at + 3] = b[1];
 }
 
-constexpr int kRT = 2;  // row tiles per wave
-constexpr int kMaxVT = 4;  // vector tiles (16 vectors each) per launch
+constexpr int kMaxVT = 4;    // vector tiles (16 vectors each) per launch
+constexpr int kMvWaves = 8;  // waves per workgroup: an eighth of the blocks each
+constexpr int kBatch = 8;    // block pairs whose loads a wave issues together
+
+// Row tiles per workgroup: one for a single vector tile (the most
+// workgroups, for the weight stream), two when several vector tiles share
+// each weight load.
+template <int NVT>
+constexpr int kRowTiles = NVT == 1 ? 1 : 2;
 
 template <int NVT>
-__global__ __launch_bounds__(256) void matvec_q8_kernel(const uint8_t *quants, const uint16_t *scales, int rows,
-                                                        int n_tiles, int n_pairs, const _Float16 *xp,
-                                                        const float *xs, int n_blocks_pad, int v0, int n_vec,
-                                                        float *y) {
+__global__ __launch_bounds__(kMvWaves * 64) void matvec_q8_kernel(const uint8_t *quants, const uint16_t *scales,
+                                                                 int rows, int n_tiles, int n_pairs,
+                                                                 const _Float16 *xp, const float *xs,
+                                                                 int n_blocks_pad, int v0, int n_vec, float *y) {
+    constexpr int RT = kRowTiles<NVT>;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int tile0 = blockIdx.x * kRT;
+    const int tile0 = blockIdx.x * RT;
     const int kg = lane >> 4;
     const int lc = lane & 15;
-    // this wave's block pairs: an even quarter of them
-    const int per = (n_pairs + 3) / 4;
+    const int per = (n_pairs + kMvWaves - 1) / kMvWaves;
     const int p0 = wave * per;
     const int p1 = min(n_pairs, p0 + per);
 
-    floatx4 acc[kRT][NVT];
+    floatx4 acc[RT][NVT];
 #pragma unroll
-    for (int rt = 0; rt < kRT; rt++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int vt = 0; vt < NVT; vt++) acc[rt][vt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int p = p0; p < p1; p++) {
-        uint4 qw[kRT], sw[kRT];
-#pragma unroll
-        for (int rt = 0; rt < kRT; rt++) {
-            const int tile = min(tile0 + rt, n_tiles - 1);
-            const int64_t tp = (int64_t)tile * n_pairs + p;
-            const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(quants + (tp * 64 + lane) * 16));
-            qw[rt] = make_uint4(q.x, q.y, q.z, q.w);
-            sw[rt] = *reinterpret_cast<const uint4 *>(scales + (tp * 16 + kg * 4) * 2);
-        }
+    // one pair of blocks: both blocks' pieces for every vector tile, then the MFMAs
+    auto pair = [&](const uint4 (&qw)[RT], const uint4 (&sw)[RT], int p) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int blk = 2 * p + j;
@@ -224,13 +235,15 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(const uint8_t *quants, c
                 bl[vt] = *reinterpret_cast<const half8 *>(src + 8);
             }
 #pragma unroll
-            for (int rt = 0; rt < kRT; rt++) {
+            for (int rt = 0; rt < RT; rt++) {
+                const uint4 q = qw[rt];
+                const uint4 sv = sw[rt];
                 half8 a;
-                bytes_to_h(j ? qw[rt].z : qw[rt].x, a, 0);
-                bytes_to_h(j ? qw[rt].w : qw[rt].y, a, 4);
+                bytes_to_h(j ? q.z : q.x, a, 0);
+                bytes_to_h(j ? q.w : q.y, a, 4);
                 // scales of rows kg*4 + r: the lane's 16 bytes hold [row][block] f16
-                const uint32_t s01 = j == 0 ? (sw[rt].x & 0xffffu) | (sw[rt].y << 16) : (sw[rt].x >> 16) | (sw[rt].y & 0xffff0000u);
-                const uint32_t s23 = j == 0 ? (sw[rt].z & 0xffffu) | (sw[rt].w << 16) : (sw[rt].z >> 16) | (sw[rt].w & 0xffff0000u);
+                const uint32_t s01 = j == 0 ? (sv.x & 0xffffu) | (sv.y << 16) : (sv.x >> 16) | (sv.y & 0xffff0000u);
+                const uint32_t s23 = j == 0 ? (sv.z & 0xffffu) | (sv.w << 16) : (sv.z >> 16) | (sv.w & 0xffff0000u);
                 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
                 const half2v h01 = __builtin_bit_cast(half2v, s01);
                 const half2v h23 = __builtin_bit_cast(half2v, s23);
@@ -245,23 +258,49 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(const uint8_t *quants, c
                 }
             }
         }
+    };
+    auto load = [&](uint4 (&qw)[RT], uint4 (&sw)[RT], int p) {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const int tile = min(tile0 + rt, n_tiles - 1);
+            const int64_t tp = (int64_t)tile * n_pairs + p;
+            const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(quants + (tp * 64 + lane) * 16));
+            qw[rt] = make_uint4(q.x, q.y, q.z, q.w);
+            sw[rt] = *reinterpret_cast<const uint4 *>(scales + (tp * 16 + kg * 4) * 2);
+        }
+    };
+
+    int pb = p0;
+    // whole batches: the batch's weight loads first (one round trip), and no
+    // branch inside, so the piece loads of later pairs can be hoisted
+    for (; pb + kBatch <= p1; pb += kBatch) {
+        uint4 qw[kBatch][RT], sw[kBatch][RT];
+#pragma unroll
+        for (int i = 0; i < kBatch; i++) load(qw[i], sw[i], pb + i);
+#pragma unroll
+        for (int i = 0; i < kBatch; i++) pair(qw[i], sw[i], pb + i);
+    }
+    for (; pb < p1; pb++) {
+        uint4 qw[RT], sw[RT];
+        load(qw, sw, pb);
+        pair(qw, sw, pb);
     }
 
-    // merge the four waves' block ranges
-    __shared__ floatx4 red[4][kRT * NVT][64];
+    // merge the waves' block ranges
+    __shared__ floatx4 red[kMvWaves][RT * NVT][64];
 #pragma unroll
-    for (int rt = 0; rt < kRT; rt++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int vt = 0; vt < NVT; vt++) red[wave][rt * NVT + vt][lane] = acc[rt][vt];
     __syncthreads();
-    for (int i = threadIdx.x; i < kRT * NVT * 64; i += 256) {
+    for (int i = threadIdx.x; i < RT * NVT * 64; i += kMvWaves * 64) {
         const int rv = i >> 6;
         const int ln = i & 63;
         const int rt = rv / NVT;
         const int vt = rv - rt * NVT;
         floatx4 s = red[0][rv][ln];
 #pragma unroll
-        for (int w = 1; w < 4; w++) s += red[w][rv][ln];
+        for (int w = 1; w < kMvWaves; w++) s += red[w][rv][ln];
         const int tile = tile0 + rt;
         const int v = v0 + vt * 16 + (ln & 15);
         if (tile >= n_tiles || v >= n_vec) continue;
@@ -274,12 +313,207 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(const uint8_t *quants, c
     }
 }
 
+// ---- few vectors: f32 on the vector ALUs -------------------------------------------
+
+constexpr int kFewWaves = 8;        // waves per workgroup: an eighth of the block pairs each
+constexpr int kFewBatch = 8;        // block pairs whose weight loads a wave issues together
+constexpr int kFewMaxVec = 4;       // vectors per launch
+constexpr int kFewLdsFloats = 16384;  // x of the launch's vectors staged in LDS (64 KiB)
+
+// x elements per thread and vector that one staging chunk loads: for
+// NV >= 2 one chunk covers the widest row that fits; one vector takes 8 at a
+// time. Each vector's LDS row is padded to whole chunks.
+__host__ __device__ constexpr int few_xc(int nv) {
+    return nv == 1 ? 8 : (kFewLdsFloats / nv + kFewWaves * 64 - 1) / (kFewWaves * 64);
+}
+__host__ __device__ constexpr int few_stride(int nv, int kpad) {
+    return (kpad + few_xc(nv) * kFewWaves * 64 - 1) / (few_xc(nv) * kFewWaves * 64) * (few_xc(nv) * kFewWaves * 64);
+}
+
+// y[v][row] for NV (1..4) vectors, one workgroup per 16-row tile: the same
+// repacked weights as the MFMA path, with f32 FMAs against x staged once in
+// LDS (no activation pieces, no padding to 16 vectors). Lane (row r, group
+// kg) covers elements kg*8 .. +8 of both blocks of a pair; each stored byte
+// q + 128 becomes the exact f32 q in one signed-byte convert (after one xor
+// per four bytes). The two block sums take the row's block scales, then the
+// four groups and the waves are summed in a fixed order. Bound: HBM on the
+// weights (34 bytes per 32).
+template <int NV>
+__global__ __launch_bounds__(kFewWaves * 64) void matvec_q8_few_kernel(const uint8_t *quants,
+                                                                      const uint16_t *scales, int rows,
+                                                                      int n_pairs, int cols, const float *x,
+                                                                      float *y) {
+    extern __shared__ float xl[];  // [NV][few_stride(NV, n_pairs * 64)], zero past cols
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tile = blockIdx.x;
+    const int kg = lane >> 4;
+    const int r = lane & 15;
+    const int per = (n_pairs + kFewWaves - 1) / kFewWaves;
+    const int p0 = min(n_pairs, wave * per);
+    const int p1 = min(n_pairs, p0 + per);
+    const int kpad = n_pairs * 64;
+    const int xstride = few_stride(NV, kpad);
+
+    auto load = [&](uint4 &q, uint32_t &sc, int p) {
+        const int64_t tp = (int64_t)tile * n_pairs + p;
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(quants + (tp * 64 + lane) * 16));
+        q = make_uint4(v.x, v.y, v.z, v.w);
+        sc = *reinterpret_cast<const uint32_t *>(scales + (tp * 16 + r) * 2);  // the row's two block scales
+    };
+    float acc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++) acc[v] = 0.0f;
+    auto pair = [&](const uint4 &q, uint32_t sc, int p) {
+        float w[16];  // q, exact
+        const uint32_t qs[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+#pragma unroll
+        for (int e = 0; e < 16; e++) w[e] = (float)(int8_t)(qs[e >> 2] >> (8 * (e & 3)));
+        typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+        const half2v s2 = __builtin_bit_cast(half2v, sc);
+        const float s0 = (float)s2[0];
+        const float s1 = (float)s2[1];
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            const float *xa = xl + v * xstride + p * 64 + kg * 8;  // block 2p
+            const float4 a0 = *reinterpret_cast<const float4 *>(xa);
+            const float4 a1 = *reinterpret_cast<const float4 *>(xa + 4);
+            const float4 b0 = *reinterpret_cast<const float4 *>(xa + 32);  // block 2p + 1
+            const float4 b1 = *reinterpret_cast<const float4 *>(xa + 36);
+            float t0 = w[0] * a0.x;
+            t0 = fmaf(w[1], a0.y, t0);
+            t0 = fmaf(w[2], a0.z, t0);
+            t0 = fmaf(w[3], a0.w, t0);
+            t0 = fmaf(w[4], a1.x, t0);
+            t0 = fmaf(w[5], a1.y, t0);
+            t0 = fmaf(w[6], a1.z, t0);
+            t0 = fmaf(w[7], a1.w, t0);
+            float t1 = w[8] * b0.x;
+            t1 = fmaf(w[9], b0.y, t1);
+            t1 = fmaf(w[10], b0.z, t1);
+            t1 = fmaf(w[11], b0.w, t1);
+            t1 = fmaf(w[12], b1.x, t1);
+            t1 = fmaf(w[13], b1.y, t1);
+            t1 = fmaf(w[14], b1.z, t1);
+            t1 = fmaf(w[15], b1.w, t1);
+            acc[v] = fmaf(t0, s0, acc[v]);
+            acc[v] = fmaf(t1, s1, acc[v]);
+        }
+    };
+
+    // x loads first, all at once into registers, then the first batch of
+    // weights: loads return in order, so writing x to LDS waits for x alone
+    // while the weights stay in flight
+    constexpr int kXC = few_xc(NV);
+    constexpr int kChunk = kXC * kFewWaves * 64;  // columns per chunk
+    // loads without branches (addresses clamped in bounds, values selected
+    // after), so the wait before the LDS writes counts the x loads alone
+    float xr[NV][kXC];
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+#pragma unroll
+        for (int u = 0; u < kXC; u++) {
+            const int c = threadIdx.x + u * kFewWaves * 64;
+            const float t = x[(int64_t)v * cols + min(c, cols - 1)];
+            xr[v][u] = c < cols ? t : 0.0f;
+        }
+    uint4 qa[kFewBatch];
+    uint32_t sa[kFewBatch];
+    const bool whole = p0 + kFewBatch <= p1;
+#pragma unroll
+    for (int i = 0; i < kFewBatch; i++) load(qa[i], sa[i], min(p0 + i, n_pairs - 1));
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+#pragma unroll
+        for (int u = 0; u < kXC; u++) xl[v * xstride + threadIdx.x + u * kFewWaves * 64] = xr[v][u];  // padded row
+    for (int c0 = kChunk; NV == 1 && c0 < kpad; c0 += kChunk) {  // rows wider than one chunk
+        float xw[NV][kXC];
+#pragma unroll
+        for (int v = 0; v < NV; v++)
+#pragma unroll
+            for (int u = 0; u < kXC; u++) {
+                const int c = c0 + threadIdx.x + u * kFewWaves * 64;
+                const float t = x[(int64_t)v * cols + min(c, cols - 1)];
+                xw[v][u] = c < cols ? t : 0.0f;
+            }
+#pragma unroll
+        for (int v = 0; v < NV; v++)
+#pragma unroll
+            for (int u = 0; u < kXC; u++) xl[v * xstride + c0 + threadIdx.x + u * kFewWaves * 64] = xw[v][u];
+    }
+    __syncthreads();
+
+    int pb = p0;
+    if (whole) {
+        for (;;) {
+            const int nb = pb + kFewBatch;
+            const bool more = nb + kFewBatch <= p1;
+            uint4 qb[kFewBatch];
+            uint32_t sb[kFewBatch];
+            if (more) {
+#pragma unroll
+                for (int i = 0; i < kFewBatch; i++) load(qb[i], sb[i], nb + i);
+            }
+#pragma unroll
+            for (int i = 0; i < kFewBatch; i++) pair(qa[i], sa[i], pb + i);
+            pb = nb;
+            if (!more) break;
+#pragma unroll
+            for (int i = 0; i < kFewBatch; i++) {
+                qa[i] = qb[i];
+                sa[i] = sb[i];
+            }
+        }
+    }
+    for (; pb < p1; pb++) {
+        uint4 q;
+        uint32_t sc;
+        load(q, sc, pb);
+        pair(q, sc, pb);
+    }
+
+    // the four element groups of each row, then the waves, in a fixed order
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        acc[v] += __shfl_xor(acc[v], 16);
+        acc[v] += __shfl_xor(acc[v], 32);
+    }
+    __syncthreads();  // x is no longer read: its LDS holds the waves' sums
+    if (lane < 16) {
+#pragma unroll
+        for (int v = 0; v < NV; v++) xl[(wave * NV + v) * 16 + r] = acc[v];
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < NV * 16) {
+        const int v = threadIdx.x >> 4;
+        const int rr = threadIdx.x & 15;
+        float sum = xl[v * 16 + rr];
+#pragma unroll
+        for (int w = 1; w < kFewWaves; w++) sum += xl[(w * NV + v) * 16 + rr];
+        const int row = tile * 16 + rr;
+        if (row < rows) y[(int64_t)v * rows + row] = sum;
+    }
+}
+
+template <int NV>
+int launch_few(gla_ctx *ctx, const gla_q8w *w, const float *x, float *y) {
+    const int kpad = w->n_pairs * 64;
+    if (NV > 1 && kpad > few_xc(NV) * kFewWaves * 64)  // the kernel stages one chunk per vector when NV > 1
+        return set_error(GLA_ERR_KERNEL, "matvec_q8_few_kernel<%d>: %d columns exceed one staging chunk", NV, kpad);
+    const size_t lds = (size_t)std::max(NV * few_stride(NV, kpad), kFewWaves * NV * 16) * sizeof(float);
+    hipLaunchKernelGGL((matvec_q8_few_kernel<NV>), dim3(w->n_tiles), dim3(kFewWaves * 64), lds, ctx->stream,
+                       w->quants, w->scales, w->rows, w->n_pairs, w->cols, x, y);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "matvec_q8_few_kernel launch: %s", hipGetErrorString(e));
+    return GLA_OK;
+}
+
 template <int NVT>
 int launch_matvec(gla_ctx *ctx, const gla_q8w *w, const _Float16 *xp, const float *xs, int n_blocks_pad, int v0,
                   int n_vec, float *y) {
-    const dim3 grid((w->n_tiles + kRT - 1) / kRT);
-    hipLaunchKernelGGL((matvec_q8_kernel<NVT>), grid, dim3(256), 0, ctx->stream, w->quants, w->scales, w->rows,
-                       w->n_tiles, w->n_pairs, xp, xs, n_blocks_pad, v0, n_vec, y);
+    const dim3 grid((w->n_tiles + kRowTiles<NVT> - 1) / kRowTiles<NVT>);
+    hipLaunchKernelGGL((matvec_q8_kernel<NVT>), grid, dim3(kMvWaves * 64), 0, ctx->stream, w->quants, w->scales,
+                       w->rows, w->n_tiles, w->n_pairs, xp, xs, n_blocks_pad, v0, n_vec, y);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "matvec_q8_kernel launch: %s", hipGetErrorString(e));
     return GLA_OK;
@@ -369,6 +603,29 @@ int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, f
     if (n_vec < 0) return set_error(GLA_ERR_INVALID, "gla_matvec_q8_0: n_vec %d < 0", n_vec);
     if (n_vec == 0) return GLA_OK;
     GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
+    const int kpad = w->n_pairs * 64;
+    const int few = std::min(kFewMaxVec, kFewLdsFloats / kpad);  // vectors per launch whose x fits in LDS
+    if (n_vec <= kFewMaxVec && few >= 1) {
+        int rc = GLA_OK;
+        for (int v0 = 0; v0 < n_vec && rc == GLA_OK; v0 += few) {
+            const float *xv = x + (int64_t)v0 * w->cols;
+            float *yv = y + (int64_t)v0 * w->rows;
+            switch (std::min(few, n_vec - v0)) {
+            case 1:
+                rc = launch_few<1>(ctx, w, xv, yv);
+                break;
+            case 2:
+                rc = launch_few<2>(ctx, w, xv, yv);
+                break;
+            case 3:
+                rc = launch_few<3>(ctx, w, xv, yv);
+                break;
+            default:
+                rc = launch_few<4>(ctx, w, xv, yv);
+            }
+        }
+        return rc;
+    }
     const int n_blocks_pad = 2 * w->n_pairs;
     const int vec_pad = (n_vec + 15) / 16 * 16;
     const size_t xp_bytes = (size_t)vec_pad * n_blocks_pad * 32 * 2 * sizeof(_Float16);  // hi + lo per element
@@ -377,8 +634,8 @@ int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, f
     if (rc != GLA_OK) return rc;
     _Float16 *xp = (_Float16 *)ctx->scratch;
     float *xs = (float *)((uint8_t *)ctx->scratch + xp_bytes);
-    hipLaunchKernelGGL(split_x_kernel, dim3(vec_pad), dim3(256), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad, xp,
-                       xs);
+    hipLaunchKernelGGL(split_x_kernel, dim3((n_blocks_pad * 4 + 255) / 256, vec_pad), dim3(256), 0, ctx->stream, x,
+                       n_vec, w->cols, n_blocks_pad, xp, xs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "split_x_kernel launch: %s", hipGetErrorString(e));
     for (int v0 = 0; v0 < n_vec; v0 += 16 * kMaxVT) {

@@ -91,8 +91,14 @@ def test_matvec_q8_0_reference_fixture(backend):
 
 
 @pytest.mark.parametrize("rows,cols,n_vec", [
-    (6144, 4096, 1),    # Llama-3-8B fused QKV projection, one token
-    (6144, 4096, 64),   # the same over a decode batch of 64
+    (6144, 4096, 1),    # Llama-3-8B fused QKV projection, one token (the vector-ALU kernel)
+    (6144, 4096, 4),    # four tokens: the largest vector-ALU launch
+    (6144, 4096, 64),   # the same over a decode batch of 64 (MFMA)
+    (96, 14336, 2),     # FFN down-projection width: x of one vector fills LDS, one launch per vector
+    (40, 16416, 1),     # 513 blocks: x too wide for LDS, a single vector on the MFMA path
+    (100, 96, 3),       # vector-ALU kernel on a row tail and an odd block count
+    (64, 4096, 3),      # three vectors: x padded to 3 x 5632 floats, 66 KiB of LDS
+    (16, 32, 2),        # one block pair: seven of the eight waves have no blocks
     (4096, 4096, 5),    # the output projection, a ragged batch
     (100, 96, 70),      # a row tail (100 = 6 x 16 + 4), an odd block count, two vector launches
     (16, 32, 17),
