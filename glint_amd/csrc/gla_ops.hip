@@ -18,12 +18,12 @@
 // (hi = f16(x * 2^s), lo = f16(x * 2^s - hi), s per vector putting the
 // largest |x| near 2^14), so each block's product runs as two MFMAs with
 // exact int8 x f16 products and f32 accumulation; the f16 block scale is
-// applied in f32 per block, as the reference applies it. A workgroup owns one
-// row tile (two when there are several vector tiles) for every vector of the
-// launch (up to 64), so the weights are read once per launch; its eight waves
-// split the blocks, each issuing the loads of eight block pairs before
-// computing them, and are merged in LDS. Bound: HBM on the weights (34 bytes
-// per 32 weights).
+// applied in f32 per block, as the reference applies it. Each launch covers
+// up to 64 vectors, so the weights are read once per 64 vectors; K is split
+// across workgroups (the slices summed in order by a second kernel) so that
+// each CU reads only its slice of the activation pieces. Up to four vectors
+// take the vector-ALU kernel instead (x in f32 from LDS, no pieces). Bound:
+// HBM on the weights (34 bytes per 32 weights).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -126,53 +126,76 @@ __global__ __launch_bounds__(256) void q8w_repack_kernel(const uint8_t *ggml, in
 
 // ---- activations: f16 pieces ---------------------------------------------------
 
-// Grid (chunks of 256 units, padded vector count); vectors past n_vec get
-// zero pieces. Each workgroup finds its vector's largest |x| itself (all of
-// the vector's loads in flight at once), then writes the pieces of its chunk:
-// xp[v][blk][kg] = {hi[8], lo[8]} for the 8 elements blk*32 + kg*8 .. +8,
-// and xs[v] = 2^-s, the factor that undoes the scaling.
-constexpr int kSplitUnroll = 8;
+// Grid (chunks of 256 * kSplitU units, padded vector count); vectors past
+// n_vec get zero pieces. Each thread holds its units' 8 elements each in
+// registers; the vector's largest |x| comes from those registers when one
+// chunk covers the vector (a second, streaming read otherwise), and the
+// pieces are written from the same registers, in the B-operand order of the
+// MFMA: xp[v / 16][blk][piece][lane = kg*16 + v % 16] = 8 f16 of elements
+// blk*32 + kg*8 .. +8 (piece 0 hi, 1 lo), so that one vector tile's piece of
+// a block is 1 KiB contiguous; xs[v] = 2^-s, the factor that undoes the
+// scaling.
+constexpr int kSplitU = 8;
+template <bool A16>  // x rows 16-byte aligned: float4 loads
 __global__ __launch_bounds__(256) void split_x_kernel(const float *x, int n_vec, int cols, int n_blocks_pad,
                                                       _Float16 *xp, float *xs) {
     const int v = blockIdx.y;
     const float *xv = x + (int64_t)min(v, n_vec - 1) * cols;
+    const int n_units = n_blocks_pad * 4;
+    const int cu = cols / 8;  // units inside the row (cols is a multiple of 32)
+    float e[kSplitU][8];
     float mx = 0.0f;
-    if (v < n_vec) {
-        for (int c0 = 0; c0 < cols; c0 += 256 * kSplitUnroll) {
-            float t[kSplitUnroll];
 #pragma unroll
-            for (int u = 0; u < kSplitUnroll; u++) {
-                const int c = c0 + threadIdx.x + u * 256;
-                t[u] = xv[min(c, cols - 1)];  // clamped: a repeat of the last element
-            }
+    for (int k = 0; k < kSplitU; k++) {
+        const int u = blockIdx.x * 256 * kSplitU + k * 256 + threadIdx.x;
+        const float *src = xv + (int64_t)min(u, cu - 1) * 8;  // clamped: loads stay in the row
+        if (A16) {
+            const float4 a = *reinterpret_cast<const float4 *>(src);
+            const float4 b = *reinterpret_cast<const float4 *>(src + 4);
+            e[k][0] = a.x, e[k][1] = a.y, e[k][2] = a.z, e[k][3] = a.w;
+            e[k][4] = b.x, e[k][5] = b.y, e[k][6] = b.z, e[k][7] = b.w;
+        } else {
 #pragma unroll
-            for (int u = 0; u < kSplitUnroll; u++) mx = fmaxf(mx, fabsf(t[u]));
+            for (int j = 0; j < 8; j++) e[k][j] = src[j];
         }
+        const bool in = v < n_vec && u < cu;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            e[k][j] = in ? e[k][j] : 0.0f;
+            mx = fmaxf(mx, fabsf(e[k][j]));
+        }
+    }
+    if (gridDim.x > 1 && v < n_vec) {  // rows wider than one chunk: the rest of the row's maximum
+        for (int c = threadIdx.x; c < cols; c += 256) mx = fmaxf(mx, fabsf(xv[c]));
     }
     __shared__ float red[4];
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    int e = 0;
-    if (mx > 0.0f && isfinite(mx)) frexpf(mx, &e);  // mx in [2^(e-1), 2^e)
-    const int sh = 14 - e;                             // the largest |x| * 2^sh lies in [2^13, 2^14)
+    int ex = 0;
+    if (mx > 0.0f && isfinite(mx)) frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+    const int sh = 14 - ex;                            // the largest |x| * 2^sh lies in [2^13, 2^14)
     const float mul = ldexpf(1.0f, sh);
     if (blockIdx.x == 0 && threadIdx.x == 0) xs[v] = ldexpf(1.0f, -sh);
-    const int u = blockIdx.x * 256 + threadIdx.x;  // (block, kg) unit of 8 elements
-    if (u >= n_blocks_pad * 4) return;
-    const int c0 = u * 8;
-    half8 hi, lo;
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const float t = (v < n_vec && c0 + k < cols) ? xv[c0 + k] * mul : 0.0f;
-        const _Float16 h = (_Float16)t;
-        hi[k] = h;
-        lo[k] = (_Float16)(t - (float)h);
+    for (int k = 0; k < kSplitU; k++) {
+        const int u = blockIdx.x * 256 * kSplitU + k * 256 + threadIdx.x;
+        if (u >= n_units) break;
+        half8 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float t = e[k][j] * mul;
+            const _Float16 h = (_Float16)t;
+            hi[j] = h;
+            lo[j] = (_Float16)(t - (float)h);
+        }
+        const int blk = u >> 2;
+        const int ln = (u & 3) * 16 + (v & 15);
+        _Float16 *dst = xp + (((int64_t)(v >> 4) * n_blocks_pad + blk) * 128 + ln) * 8;
+        *reinterpret_cast<half8 *>(dst) = hi;
+        *reinterpret_cast<half8 *>(dst + 64 * 8) = lo;
     }
-    _Float16 *dst = xp + ((int64_t)v * n_blocks_pad * 4 + u) * 16;
-    *reinterpret_cast<half8 *>(dst) = hi;
-    *reinterpret_cast<half8 *>(dst + 8) = lo;
 }
 
 // ---- the matvec ----------------------------------------------------------------------
@@ -191,30 +214,38 @@ __device__ __forceinline__ void bytes_to_h(uint32_t u, half8 &o, int at) {
     o[at + 3] = b[1];
 }
 
-constexpr int kMaxVT = 4;    // vector tiles (16 vectors each) per launch
-constexpr int kMvWaves = 8;  // waves per workgroup: an eighth of the blocks each
-constexpr int kBatch = 8;    // block pairs whose loads a wave issues together
+constexpr int kMaxVT = 4;        // vector tiles (16 vectors each) per launch
+constexpr int kSkWaves = 4;      // waves per workgroup: a quarter of the workgroup's blocks each
+constexpr int kSkRT = 4;         // row tiles per wave (and per workgroup): 64 rows share each x fragment
+constexpr int kSkMaxSplits = 8;  // K slices per launch (partials summed by matvec_reduce_kernel)
+constexpr int kSkTargetWgs = 512;
 
-// Row tiles per workgroup: one for a single vector tile (the most
-// workgroups, for the weight stream), two when several vector tiles share
-// each weight load.
+// One K slice of y[v][row] for up to 64 vectors: workgroup (g, s) owns rows
+// g*64 .. +64 and the block pairs of slice s, which its four waves split; each
+// wave holds 4 row tiles x NVT vector tiles of accumulators, so every x
+// fragment it loads serves four row tiles and every weight fragment NVT
+// vector tiles. The waves are merged in LDS in a fixed order and the slice's
+// sums (times the vector's piece factor) go to out[s][vv][row], or straight
+// to y when there is one slice. Splitting K across workgroups is what keeps
+// the x fragments each CU reads to its slice of x, not all of it.
 template <int NVT>
-constexpr int kRowTiles = NVT == 1 ? 1 : 2;
-
-template <int NVT>
-__global__ __launch_bounds__(kMvWaves * 64) void matvec_q8_kernel(const uint8_t *quants, const uint16_t *scales,
-                                                                 int rows, int n_tiles, int n_pairs,
-                                                                 const _Float16 *xp, const float *xs,
-                                                                 int n_blocks_pad, int v0, int n_vec, float *y) {
-    constexpr int RT = kRowTiles<NVT>;
+__global__ __launch_bounds__(kSkWaves * 64) void matvec_q8_splitk_kernel(
+    const uint8_t *quants, const uint16_t *scales, int rows, int n_tiles, int n_pairs, const _Float16 *xp,
+    const float *xs, int n_blocks_pad, int v0, int n_vec, int n_splits, float *out, int64_t split_stride) {
+    constexpr int RT = kSkRT;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int tile0 = blockIdx.x * RT;
     const int kg = lane >> 4;
-    const int lc = lane & 15;
-    const int per = (n_pairs + kMvWaves - 1) / kMvWaves;
-    const int p0 = wave * per;
-    const int p1 = min(n_pairs, p0 + per);
+    const int ps = (n_pairs + n_splits - 1) / n_splits;
+    const int q0 = min(n_pairs, (int)blockIdx.y * ps);
+    const int q1 = min(n_pairs, q0 + ps);
+    const int per = (q1 - q0 + kSkWaves - 1) / kSkWaves;
+    const int p0 = min(q1, q0 + wave * per);
+    const int p1 = min(q1, p0 + per);
+
+    __shared__ float xsl[NVT * 16];  // the launch's piece factors, read by the epilogue
+    if ((int)threadIdx.x < NVT * 16) xsl[threadIdx.x] = xs[v0 + threadIdx.x];
 
     floatx4 acc[RT][NVT];
 #pragma unroll
@@ -222,44 +253,17 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_q8_kernel(const uint8_t 
 #pragma unroll
         for (int vt = 0; vt < NVT; vt++) acc[rt][vt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // one pair of blocks: both blocks' pieces for every vector tile, then the MFMAs
-    auto pair = [&](const uint4 (&qw)[RT], const uint4 (&sw)[RT], int p) {
+    // the x pieces of one block for every vector tile: 1 KiB contiguous per piece
+    auto load_x = [&](half8 (&bh)[NVT], half8 (&bl)[NVT], int blk) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int blk = 2 * p + j;
-            half8 bh[NVT], bl[NVT];
-#pragma unroll
-            for (int vt = 0; vt < NVT; vt++) {
-                const _Float16 *src = xp + ((int64_t)(v0 + vt * 16 + lc) * n_blocks_pad * 4 + blk * 4 + kg) * 16;
-                bh[vt] = *reinterpret_cast<const half8 *>(src);
-                bl[vt] = *reinterpret_cast<const half8 *>(src + 8);
-            }
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
-                const uint4 q = qw[rt];
-                const uint4 sv = sw[rt];
-                half8 a;
-                bytes_to_h(j ? q.z : q.x, a, 0);
-                bytes_to_h(j ? q.w : q.y, a, 4);
-                // scales of rows kg*4 + r: the lane's 16 bytes hold [row][block] f16
-                const uint32_t s01 = j == 0 ? (sv.x & 0xffffu) | (sv.y << 16) : (sv.x >> 16) | (sv.y & 0xffff0000u);
-                const uint32_t s23 = j == 0 ? (sv.z & 0xffffu) | (sv.w << 16) : (sv.z >> 16) | (sv.w & 0xffff0000u);
-                typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-                const half2v h01 = __builtin_bit_cast(half2v, s01);
-                const half2v h23 = __builtin_bit_cast(half2v, s23);
-                const float sc[4] = {(float)h01[0], (float)h01[1], (float)h23[0], (float)h23[1]};
-#pragma unroll
-                for (int vt = 0; vt < NVT; vt++) {
-                    floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh[vt], floatx4{0.0f, 0.0f, 0.0f, 0.0f},
-                                                                      0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl[vt], c, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) acc[rt][vt][r] = fmaf(c[r], sc[r], acc[rt][vt][r]);
-                }
-            }
+        for (int vt = 0; vt < NVT; vt++) {
+            const _Float16 *src = xp + (((int64_t)(v0 / 16 + vt) * n_blocks_pad + blk) * 128 + lane) * 8;
+            bh[vt] = *reinterpret_cast<const half8 *>(src);
+            bl[vt] = *reinterpret_cast<const half8 *>(src + 64 * 8);
         }
     };
-    auto load = [&](uint4 (&qw)[RT], uint4 (&sw)[RT], int p) {
+    // the weights and scales of one block pair for every row tile
+    auto load_w = [&](uint4 (&qw)[RT], uint4 (&sw)[RT], int p) {
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             const int tile = min(tile0 + rt, n_tiles - 1);
@@ -269,48 +273,110 @@ __global__ __launch_bounds__(kMvWaves * 64) void matvec_q8_kernel(const uint8_t 
             sw[rt] = *reinterpret_cast<const uint4 *>(scales + (tp * 16 + kg * 4) * 2);
         }
     };
+    // block j of the pair in (qw, sw) against the pieces (bh, bl)
+    auto block = [&](const uint4 (&qw)[RT], const uint4 (&sw)[RT], const half8 (&bh)[NVT], const half8 (&bl)[NVT],
+                     int j) {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const uint4 q = qw[rt];
+            const uint4 sv = sw[rt];
+            half8 a;
+            bytes_to_h(j ? q.z : q.x, a, 0);
+            bytes_to_h(j ? q.w : q.y, a, 4);
+            // scales of rows kg*4 + r: the lane's 16 bytes hold [row][block] f16
+            const uint32_t s01 = j == 0 ? (sv.x & 0xffffu) | (sv.y << 16) : (sv.x >> 16) | (sv.y & 0xffff0000u);
+            const uint32_t s23 = j == 0 ? (sv.z & 0xffffu) | (sv.w << 16) : (sv.z >> 16) | (sv.w & 0xffff0000u);
+            typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+            const half2v h01 = __builtin_bit_cast(half2v, s01);
+            const half2v h23 = __builtin_bit_cast(half2v, s23);
+            const float sc[4] = {(float)h01[0], (float)h01[1], (float)h23[0], (float)h23[1]};
+#pragma unroll
+            for (int vt = 0; vt < NVT; vt++) {
+                floatx4 c =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh[vt], floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl[vt], c, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[rt][vt][r] = fmaf(c[r], sc[r], acc[rt][vt][r]);
+            }
+        }
+    };
 
-    int pb = p0;
-    // whole batches: the batch's weight loads first (one round trip), and no
-    // branch inside, so the piece loads of later pairs can be hoisted
-    for (; pb + kBatch <= p1; pb += kBatch) {
-        uint4 qw[kBatch][RT], sw[kBatch][RT];
-#pragma unroll
-        for (int i = 0; i < kBatch; i++) load(qw[i], sw[i], pb + i);
-#pragma unroll
-        for (int i = 0; i < kBatch; i++) pair(qw[i], sw[i], pb + i);
-    }
-    for (; pb < p1; pb++) {
+    // software pipeline: the x pieces one block ahead, the weights one pair
+    // ahead; every load is unconditional (indices clamped into the wave's
+    // range), so none is held back behind a branch
+    if (p0 < p1) {
         uint4 qw[RT], sw[RT];
-        load(qw, sw, pb);
-        pair(qw, sw, pb);
+        half8 bh[NVT], bl[NVT];
+        load_w(qw, sw, p0);
+        load_x(bh, bl, 2 * p0);
+        for (int p = p0; p < p1; p++) {
+            const int pn = min(p + 1, p1 - 1);
+            uint4 qn[RT], sn[RT];
+            half8 nh[NVT], nl[NVT];
+            load_w(qn, sn, pn);
+            load_x(nh, nl, 2 * p + 1);
+            block(qw, sw, bh, bl, 0);
+            load_x(bh, bl, 2 * pn);
+            block(qw, sw, nh, nl, 1);
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                qw[rt] = qn[rt];
+                sw[rt] = sn[rt];
+            }
+        }
     }
 
-    // merge the waves' block ranges
-    __shared__ floatx4 red[kMvWaves][RT * NVT][64];
+    // merge the waves' block ranges in a fixed order
+    __shared__ floatx4 red[kSkWaves][RT * NVT][64];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int vt = 0; vt < NVT; vt++) red[wave][rt * NVT + vt][lane] = acc[rt][vt];
     __syncthreads();
-    for (int i = threadIdx.x; i < RT * NVT * 64; i += kMvWaves * 64) {
-        const int rv = i >> 6;
-        const int ln = i & 63;
-        const int rt = rv / NVT;
-        const int vt = rv - rt * NVT;
-        floatx4 s = red[0][rv][ln];
+    float *o = out + (int64_t)blockIdx.y * split_stride;
+    for (int i = threadIdx.x; i < RT * 16 * NVT * 16; i += kSkWaves * 64) {
+        const int rl = i & (RT * 16 - 1);  // row in the workgroup: consecutive threads, consecutive rows
+        const int vv = i / (RT * 16);      // vector of the launch
+        const int rt = rl >> 4;
+        const int rr = rl & 15;
+        const int vt = vv >> 4;
+        const int ln = (rr >> 2) * 16 + (vv & 15);  // the C lane of (row rr, vector vv & 15)
+        const int r = rr & 3;
+        float sum = red[0][rt * NVT + vt][ln][r];
 #pragma unroll
-        for (int w = 1; w < kMvWaves; w++) s += red[w][rv][ln];
-        const int tile = tile0 + rt;
-        const int v = v0 + vt * 16 + (ln & 15);
-        if (tile >= n_tiles || v >= n_vec) continue;
-        const float f = xs[v];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int row = tile * 16 + (ln >> 4) * 4 + r;
-            if (row < rows) y[(int64_t)v * rows + row] = s[r] * f;
-        }
+        for (int w = 1; w < kSkWaves; w++) sum += red[w][rt * NVT + vt][ln][r];
+        const int row = tile0 * 16 + rl;
+        const int v = v0 + vv;
+        if (row < rows && v < n_vec) o[(int64_t)vv * rows + row] = sum * xsl[vv];
     }
+}
+
+// y[vv][row] = sum over the slices s = 0, 1, .. of part[s][vv][row], in order
+// (all slices' loads in flight at once).
+__global__ __launch_bounds__(256) void matvec_reduce_kernel(const float *part, int n_splits, int64_t split_stride,
+                                                            int64_t n_out, float *y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n_out) return;
+    float t[kSkMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kSkMaxSplits; s++) t[s] = part[min(s, n_splits - 1) * split_stride + i];
+    float sum = t[0];
+#pragma unroll
+    for (int s = 1; s < kSkMaxSplits; s++)
+        if (s < n_splits) sum += t[s];
+    y[i] = sum;
+}
+
+template <int NVT>
+int launch_splitk(gla_ctx *ctx, const gla_q8w *w, const _Float16 *xp, const float *xs, int n_blocks_pad, int v0,
+                  int n_vec, int n_splits, float *out, int64_t split_stride) {
+    const dim3 grid((w->n_tiles + kSkRT - 1) / kSkRT, n_splits);
+    hipLaunchKernelGGL((matvec_q8_splitk_kernel<NVT>), grid, dim3(kSkWaves * 64), 0, ctx->stream, w->quants,
+                       w->scales, w->rows, w->n_tiles, w->n_pairs, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out,
+                       split_stride);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "matvec_q8_splitk_kernel launch: %s", hipGetErrorString(e));
+    return GLA_OK;
 }
 
 // ---- few vectors: f32 on the vector ALUs -------------------------------------------
@@ -508,16 +574,6 @@ int launch_few(gla_ctx *ctx, const gla_q8w *w, const float *x, float *y) {
     return GLA_OK;
 }
 
-template <int NVT>
-int launch_matvec(gla_ctx *ctx, const gla_q8w *w, const _Float16 *xp, const float *xs, int n_blocks_pad, int v0,
-                  int n_vec, float *y) {
-    const dim3 grid((w->n_tiles + kRowTiles<NVT> - 1) / kRowTiles<NVT>);
-    hipLaunchKernelGGL((matvec_q8_kernel<NVT>), grid, dim3(kMvWaves * 64), 0, ctx->stream, w->quants, w->scales,
-                       w->rows, w->n_tiles, w->n_pairs, xp, xs, n_blocks_pad, v0, n_vec, y);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "matvec_q8_kernel launch: %s", hipGetErrorString(e));
-    return GLA_OK;
-}
 
 int64_t grid_for(int64_t n) { return (n + 255) / 256; }
 
@@ -628,32 +684,53 @@ int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, f
     }
     const int n_blocks_pad = 2 * w->n_pairs;
     const int vec_pad = (n_vec + 15) / 16 * 16;
+    const int n_groups = (w->n_tiles + kSkRT - 1) / kSkRT;
+    // K slices: enough workgroups to fill the chip, at least one block pair per wave
+    const int n_splits = std::max(1, std::min({kSkMaxSplits, (kSkTargetWgs + n_groups / 2) / n_groups,
+                                               w->n_pairs / kSkWaves}));
     const size_t xp_bytes = (size_t)vec_pad * n_blocks_pad * 32 * 2 * sizeof(_Float16);  // hi + lo per element
-    const size_t total = xp_bytes + (size_t)vec_pad * sizeof(float);
-    int rc = ensure_scratch(ctx, total);
+    const size_t xs_bytes = ((size_t)vec_pad * sizeof(float) + 255) / 256 * 256;
+    const int64_t split_stride = (int64_t)16 * kMaxVT * w->rows;  // one slice of partials: 64 vectors x rows
+    const size_t part_bytes = n_splits > 1 ? (size_t)n_splits * split_stride * sizeof(float) : 0;
+    int rc = ensure_scratch(ctx, xp_bytes + xs_bytes + part_bytes);
     if (rc != GLA_OK) return rc;
     _Float16 *xp = (_Float16 *)ctx->scratch;
     float *xs = (float *)((uint8_t *)ctx->scratch + xp_bytes);
-    hipLaunchKernelGGL(split_x_kernel, dim3((n_blocks_pad * 4 + 255) / 256, vec_pad), dim3(256), 0, ctx->stream, x,
-                       n_vec, w->cols, n_blocks_pad, xp, xs);
+    float *part = (float *)((uint8_t *)ctx->scratch + xp_bytes + xs_bytes);
+    const dim3 sgrid((n_blocks_pad * 4 + 256 * kSplitU - 1) / (256 * kSplitU), vec_pad);
+    if (((uintptr_t)x & 15) == 0)  // rows start 128-byte apart: the base decides
+        hipLaunchKernelGGL(split_x_kernel<true>, sgrid, dim3(256), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad,
+                           xp, xs);
+    else
+        hipLaunchKernelGGL(split_x_kernel<false>, sgrid, dim3(256), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad,
+                           xp, xs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "split_x_kernel launch: %s", hipGetErrorString(e));
     for (int v0 = 0; v0 < n_vec; v0 += 16 * kMaxVT) {
         const int nvt = std::min(kMaxVT, (n_vec - v0 + 15) / 16);
+        float *yv = y + (int64_t)v0 * w->rows;
+        float *out = n_splits > 1 ? part : yv;
         switch (nvt) {
         case 1:
-            rc = launch_matvec<1>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, y);
+            rc = launch_splitk<1>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride);
             break;
         case 2:
-            rc = launch_matvec<2>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, y);
+            rc = launch_splitk<2>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride);
             break;
         case 3:
-            rc = launch_matvec<3>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, y);
+            rc = launch_splitk<3>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride);
             break;
         default:
-            rc = launch_matvec<4>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, y);
+            rc = launch_splitk<4>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride);
         }
         if (rc != GLA_OK) return rc;
+        if (n_splits > 1) {
+            const int64_t n_out = (int64_t)std::min(16 * kMaxVT, n_vec - v0) * w->rows;
+            hipLaunchKernelGGL(matvec_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, ctx->stream,
+                               part, n_splits, split_stride, n_out, yv);
+            e = hipGetLastError();
+            if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "matvec_reduce_kernel launch: %s", hipGetErrorString(e));
+        }
     }
     return GLA_OK;
 }
