@@ -587,11 +587,11 @@ extern "C" {
 int gla_rope(gla_ctx *ctx, float *x, int n_rows, int n_heads, int head_dim, const int32_t *pos, float freq_base,
              float scaling_factor, int rot_dim) {
     if (!ctx || (!x && n_rows > 0) || (!pos && n_rows > 0)) return set_error(GLA_ERR_INVALID, "gla_rope: NULL argument");
-    if (n_rows < 0 || n_heads <= 0 || head_dim <= 0 || head_dim % 2 || rot_dim < 0)
+    // as the reference: an odd head_dim leaves its last dimension alone, and
+    // freq_base / scaling_factor are not checked (0 or negative give inf/NaN there too)
+    if (n_rows < 0 || n_heads <= 0 || head_dim <= 0 || rot_dim < 0)
         return set_error(GLA_ERR_INVALID, "gla_rope: bad shape (rows %d, heads %d, head_dim %d, rot_dim %d)", n_rows,
                          n_heads, head_dim, rot_dim);
-    if (!(freq_base > 0.0f) || !(scaling_factor > 0.0f))
-        return set_error(GLA_ERR_INVALID, "gla_rope: freq_base and scaling_factor must be positive");
     const int rot = std::min(rot_dim, head_dim) & ~1;
     const int n_pairs = rot / 2;
     if (n_rows == 0 || n_pairs == 0) return GLA_OK;

@@ -747,7 +747,7 @@ struct GpuBackend::Staging {
         void *ptr = nullptr;
         size_t bytes = 0;
     };
-    enum { Q, OUT, TABLE, START, LEN, SLOT, QSTART, POSOFF, N_BUFS };
+    enum { Q, OUT, TABLE, START, LEN, SLOT, QSTART, POSOFF, POS, N_BUFS };
     std::shared_ptr<Device> dev;
     Buf bufs[N_BUFS];
 
@@ -1054,6 +1054,79 @@ Result<std::vector<float>> GpuBackend::prefill_batch(const std::vector<PrefillSe
     s = check(gla_memcpy_dtoh(dev_->ctx(), out.data(), a.out, out.size() * sizeof(float)), "gla_memcpy_dtoh");
     if (!s) return s.error();
     return out;
+}
+
+// ---- the ops beside attention ------------------------------------------------------------
+
+GpuQ8Weights::GpuQ8Weights(std::shared_ptr<Device> dev, gla_q8w *w, size_t rows, size_t cols)
+    : dev_(std::move(dev)), w_(w), rows_(rows), cols_(cols) {}
+GpuQ8Weights::GpuQ8Weights(GpuQ8Weights &&o) noexcept
+    : dev_(std::move(o.dev_)), w_(o.w_), rows_(o.rows_), cols_(o.cols_) {
+    o.w_ = nullptr;
+}
+GpuQ8Weights &GpuQ8Weights::operator=(GpuQ8Weights &&o) noexcept {
+    if (this != &o) {
+        if (w_) gla_q8w_destroy(w_);
+        dev_ = std::move(o.dev_);
+        w_ = o.w_;
+        rows_ = o.rows_;
+        cols_ = o.cols_;
+        o.w_ = nullptr;
+    }
+    return *this;
+}
+GpuQ8Weights::~GpuQ8Weights() {
+    if (w_) gla_q8w_destroy(w_);
+}
+
+Result<GpuQ8Weights> GpuBackend::upload_q8_0(const uint8_t *ggml, size_t n_bytes, size_t rows, size_t cols) {
+    if (cols % 32 != 0 || rows == 0 || cols == 0 || rows > INT32_MAX || cols > INT32_MAX)
+        return GlintError::gpu_buffer_error(fmt("upload_q8_0: %zu x %zu is not a Q8_0 matrix", rows, cols));
+    if (n_bytes != rows * (cols / 32) * 34)
+        return GlintError::gpu_buffer_error(
+            fmt("upload_q8_0: %zu bytes for %zu x %zu (expected %zu)", n_bytes, rows, cols, rows * (cols / 32) * 34));
+    gla_q8w *w = nullptr;
+    Status s = check(gla_q8w_create(dev_->ctx(), ggml, (int)rows, (int)cols, &w), "gla_q8w_create");
+    if (!s) return s.error();
+    return GpuQ8Weights(dev_, w, rows, cols);
+}
+
+Result<std::vector<float>> GpuBackend::matvec_q8_0(const GpuQ8Weights &w, const float *x, size_t n_vec) {
+    if (!w.handle()) return GlintError::gpu_shader_error("matvec_q8_0: weights not uploaded");
+    if (n_vec == 0) return std::vector<float>();
+    if (n_vec > INT32_MAX) return GlintError::gpu_shader_error("matvec_q8_0: too many vectors");
+    Staging &st = *stage_;
+    Result<void *> px = st.put(Staging::Q, x, n_vec * w.cols() * sizeof(float));
+    if (!px) return px.error();
+    Result<void *> py = st.get(Staging::OUT, n_vec * w.rows() * sizeof(float));
+    if (!py) return py.error();
+    Status s = check(gla_matvec_q8_0(dev_->ctx(), w.handle(), (const float *)px.value(), (int)n_vec,
+                                     (float *)py.value()),
+                     "gla_matvec_q8_0");
+    if (!s) return s.error();
+    std::vector<float> y(n_vec * w.rows());
+    s = check(gla_memcpy_dtoh(dev_->ctx(), y.data(), py.value(), y.size() * sizeof(float)), "gla_memcpy_dtoh");
+    if (!s) return s.error();
+    return y;
+}
+
+Status GpuBackend::rope(float *x, size_t n_rows, size_t n_heads, size_t head_dim, const int32_t *pos,
+                        float freq_base, float scaling_factor, size_t rot_dim) {
+    if (n_rows == 0) return {};
+    if (n_rows > INT32_MAX || n_heads > INT32_MAX || head_dim > INT32_MAX)
+        return GlintError::gpu_shader_error("rope: shape out of range");
+    const size_t bytes = n_rows * n_heads * head_dim * sizeof(float);
+    Staging &st = *stage_;
+    Result<void *> px = st.put(Staging::Q, x, bytes);
+    if (!px) return px.error();
+    Result<void *> pp = st.put(Staging::POS, pos, n_rows * sizeof(int32_t));
+    if (!pp) return pp.error();
+    Status s = check(gla_rope(dev_->ctx(), (float *)px.value(), (int)n_rows, (int)n_heads, (int)head_dim,
+                              (const int32_t *)pp.value(), freq_base, scaling_factor,
+                              (int)std::min<size_t>(rot_dim, INT32_MAX)),
+                     "gla_rope");
+    if (!s) return s;
+    return check(gla_memcpy_dtoh(dev_->ctx(), x, px.value(), bytes), "gla_memcpy_dtoh");
 }
 
 size_t window_start(size_t pos, size_t sliding_window, bool alternating, size_t layer) {

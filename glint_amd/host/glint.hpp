@@ -497,6 +497,29 @@ struct AttnShape {
     float softcap = 0.0f;  // attn_logit_softcapping; 0: none
 };
 
+// GGML Q8_0 weights on the device: the buffer QuantizedTensor::upload_to_gpu
+// puts there (src/tensor/quantized.rs:398-401, GpuBackend::upload_buffer
+// src/backend/gpu.rs:111-121), repacked once for the device matvec. Move-only;
+// frees the device copy when dropped.
+class GpuQ8Weights {
+  public:
+    GpuQ8Weights(GpuQ8Weights &&o) noexcept;
+    GpuQ8Weights &operator=(GpuQ8Weights &&o) noexcept;
+    GpuQ8Weights(const GpuQ8Weights &) = delete;
+    GpuQ8Weights &operator=(const GpuQ8Weights &) = delete;
+    ~GpuQ8Weights();
+    size_t rows() const { return rows_; }
+    size_t cols() const { return cols_; }
+    const gla_q8w *handle() const { return w_; }
+
+  private:
+    friend class GpuBackend;
+    GpuQ8Weights(std::shared_ptr<Device> dev, gla_q8w *w, size_t rows, size_t cols);
+    std::shared_ptr<Device> dev_;
+    gla_q8w *w_ = nullptr;
+    size_t rows_ = 0, cols_ = 0;
+};
+
 class GpuBackend {
   public:
     // GpuBackend::new (src/backend/gpu.rs:44-99): GpuAdapterNotFound when no
@@ -546,6 +569,19 @@ class GpuBackend {
     Result<std::vector<float>> prefill_batch(const std::vector<PrefillSeq> &seqs, const float *q, size_t layer,
                                              const AttnShape &shape, size_t sliding_window = 0,
                                              gla_precision precision = GLA_PREC_F32);
+
+    // The ops beside attention on a decode step.
+    // QuantizedTensor::upload_to_gpu of a Q8_0 tensor: ggml holds rows x
+    // cols/32 blocks of [f16 scale][32 x i8] (n_bytes = rows * cols / 32 * 34).
+    Result<GpuQ8Weights> upload_q8_0(const uint8_t *ggml, size_t n_bytes, size_t rows, size_t cols);
+    // GpuBackend::matvec_q8_0 (src/backend/gpu.rs:204-213) and
+    // QuantizedTensor::matvec_batch (src/tensor/quantized.rs:302-346) in one
+    // call: x [n_vec][cols] host -> [n_vec][rows].
+    Result<std::vector<float>> matvec_q8_0(const GpuQ8Weights &w, const float *x, size_t n_vec);
+    // tensor::rope (src/tensor/ops.rs:212-245) over n_rows rows of n_heads
+    // heads, row r at position pos[r], in place on host data.
+    Status rope(float *x, size_t n_rows, size_t n_heads, size_t head_dim, const int32_t *pos, float freq_base,
+                float scaling_factor, size_t rot_dim);
 
   private:
     explicit GpuBackend(std::shared_ptr<Device> dev);

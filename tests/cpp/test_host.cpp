@@ -1162,6 +1162,138 @@ DEVICE_TEST(test_fixed_caches_reserve_is_a_noop) {
     CHECK(plain.reserve(1000000).ok());
 }
 
+// ---- the ops beside attention (src/tensor/quantized.rs, src/tensor/ops.rs) -----------------
+
+// One GGML Q8_0 block: [f16 scale LE][32 x i8].
+void push_block(std::vector<uint8_t> &out, uint16_t scale_bits, const int8_t *q) {
+    out.push_back((uint8_t)(scale_bits & 0xff));
+    out.push_back((uint8_t)(scale_bits >> 8));
+    for (int j = 0; j < 32; j++) out.push_back((uint8_t)q[j]);
+}
+
+// quantized.rs test_q8_0_matvec_matches_f32: rows [0..31] x scale 1.0 and
+// [0, -1, .., -31] x scale 2.0 against [0..31] give 10416 and -20832 (exact:
+// integer products and sums below 2^24).
+DEVICE_TEST(test_matvec_q8_0_reference_fixture) {
+    std::vector<uint8_t> raw;
+    int8_t a[32], b[32];
+    for (int j = 0; j < 32; j++) a[j] = (int8_t)j, b[j] = (int8_t)-j;
+    push_block(raw, 0x3C00, a);  // 1.0
+    push_block(raw, 0x4000, b);  // 2.0
+    auto w = backend().upload_q8_0(raw.data(), raw.size(), 2, 32).expect("upload");
+    CHECK_EQ(w.rows(), 2u);
+    CHECK_EQ(w.cols(), 32u);
+    std::vector<float> x(32);
+    for (int j = 0; j < 32; j++) x[j] = (float)j;
+    const auto y = backend().matvec_q8_0(w, x.data(), 1).expect("matvec");
+    CHECK_EQ(y.size(), 2u);
+    CHECK_EQ(y[0], 10416.0f);
+    CHECK_EQ(y[1], -20832.0f);
+}
+
+// Random Q8_0 matrices (row tails, odd block counts, the vector-ALU and the
+// MFMA paths) against the f64 product of the dequantised rows: within 2e-6
+// of sum |x * w| per output.
+DEVICE_TEST(test_matvec_q8_0_matches_f64) {
+    struct Shape {
+        size_t rows, cols, n_vec;
+    };
+    const Shape shapes[] = {{100, 96, 3}, {64, 4096, 1}, {48, 512, 20}, {16, 32, 70}};
+    Rng rng(0x0a7e);
+    for (const Shape &sh : shapes) {
+        const size_t nb = sh.cols / 32;
+        std::vector<uint8_t> raw;
+        std::vector<double> wd(sh.rows * sh.cols);
+        for (size_t r = 0; r < sh.rows; r++)
+            for (size_t blk = 0; blk < nb; blk++) {
+                int8_t q[32];
+                for (int j = 0; j < 32; j++) q[j] = (int8_t)((int)(rng.uniform() * 255.0) - 127);
+                // a normal f16 in [2^-12, 2^-2): exponent field 3..12, random mantissa
+                const uint16_t bits = (uint16_t)(((3 + (int)(rng.uniform() * 10.0)) << 10) | (int)(rng.uniform() * 1024.0));
+                push_block(raw, bits, q);
+                const double sc = f16_to_f32(bits);
+                for (int j = 0; j < 32; j++) wd[r * sh.cols + blk * 32 + j] = sc * q[j];
+            }
+        auto w = backend().upload_q8_0(raw.data(), raw.size(), sh.rows, sh.cols).expect("upload");
+        const auto x = rng.normal(sh.n_vec * sh.cols);
+        const auto y = backend().matvec_q8_0(w, x.data(), sh.n_vec).expect("matvec");
+        CHECK_EQ(y.size(), sh.n_vec * sh.rows);
+        for (size_t v = 0; v < sh.n_vec; v++)
+            for (size_t r = 0; r < sh.rows; r++) {
+                double exact = 0.0, mag = 0.0;
+                for (size_t c = 0; c < sh.cols; c++) {
+                    exact += (double)x[v * sh.cols + c] * wd[r * sh.cols + c];
+                    mag += std::fabs((double)x[v * sh.cols + c] * wd[r * sh.cols + c]);
+                }
+                CHECK_MSG(std::fabs(y[v * sh.rows + r] - exact) <= 2e-6 * mag,
+                          sh.rows << "x" << sh.cols << " vec " << v << " row " << r << ": " << y[v * sh.rows + r]
+                                  << " vs " << exact);
+            }
+    }
+}
+
+DEVICE_TEST(test_upload_q8_0_rejects_bad_sizes) {
+    std::vector<uint8_t> raw(34 * 4, 0);
+    CHECK(!backend().upload_q8_0(raw.data(), raw.size(), 2, 48).ok());      // cols not a multiple of 32
+    CHECK(!backend().upload_q8_0(raw.data(), raw.size() - 1, 2, 64).ok());  // short buffer
+    auto w = backend().upload_q8_0(raw.data(), raw.size(), 2, 64).expect("upload");
+    auto moved = std::move(w);
+    CHECK(moved.handle() != nullptr);
+    CHECK(w.handle() == nullptr);
+}
+
+// ops.rs tests through the host layer: position 0 is the identity (full and
+// partial rotary); pos 2 at scaling 2 equals pos 1 at scaling 1 bit for bit;
+// dimensions past rot_dim (and an odd head_dim's last one) are untouched; and
+// the rotation against the f64 one, within the f32 angle's own rounding.
+DEVICE_TEST(test_rope_through_host_layer) {
+    {
+        std::vector<float> x = {1.0f, 2.0f, 3.0f, 4.0f};
+        const int32_t p0 = 0;
+        for (size_t rot : {4, 2}) {
+            std::vector<float> y = x;
+            backend().rope(y.data(), 1, 1, 4, &p0, 10000.0f, 1.0f, rot).expect("rope");
+            CHECK(y == x);
+        }
+        std::vector<float> a = x, b = x;
+        const int32_t p2 = 2, p1 = 1;
+        backend().rope(a.data(), 1, 1, 4, &p2, 10000.0f, 2.0f, 4).expect("rope");
+        backend().rope(b.data(), 1, 1, 4, &p1, 10000.0f, 1.0f, 4).expect("rope");
+        CHECK(a == b);
+    }
+    const size_t heads = 3;
+    const int32_t pos[] = {0, 1, 17, 4095, 65535};
+    const size_t n_rows = sizeof(pos) / sizeof(pos[0]);
+    struct Case {
+        size_t head_dim, rot_dim;
+        float base, scaling;
+    };
+    const Case cases_[] = {{8, 8, 10000.0f, 1.0f}, {8, 6, 500000.0f, 2.0f}, {5, 5, 10000.0f, 1.0f}};
+    Rng rng(0x20be);
+    for (const Case &c : cases_) {
+        const auto x = rng.normal(n_rows * heads * c.head_dim);
+        std::vector<float> y = x;
+        backend().rope(y.data(), n_rows, heads, c.head_dim, pos, c.base, c.scaling, c.rot_dim).expect("rope");
+        const size_t rot = std::min(c.rot_dim, c.head_dim) & ~(size_t)1;
+        for (size_t r = 0; r < n_rows; r++)
+            for (size_t h = 0; h < heads; h++) {
+                const size_t o = (r * heads + h) * c.head_dim;
+                for (size_t i = rot; i < c.head_dim; i++) CHECK(y[o + i] == x[o + i]);
+                const double ps = (double)pos[r] / c.scaling;
+                for (size_t i = 0; i < rot; i += 2) {
+                    const double ang = ps * std::pow((double)c.base, -(double)i / (double)c.head_dim);
+                    const double w0 = x[o + i] * std::cos(ang) - x[o + i + 1] * std::sin(ang);
+                    const double w1 = x[o + i] * std::sin(ang) + x[o + i + 1] * std::cos(ang);
+                    // f32 angles carry up to ~ps * 2^-23 rad of rounding
+                    const double tol = (2e-6 + ps * 2.4e-7) * (std::fabs(x[o + i]) + std::fabs(x[o + i + 1]));
+                    CHECK_MSG(std::fabs(y[o + i] - w0) <= tol && std::fabs(y[o + i + 1] - w1) <= tol,
+                              "hd " << c.head_dim << " pos " << pos[r] << " i " << i << ": " << y[o + i] << ","
+                                    << y[o + i + 1] << " vs " << w0 << "," << w1);
+                }
+            }
+    }
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {

@@ -40,6 +40,7 @@ def test_rope_reference_known_answers(backend):
 
 
 @pytest.mark.parametrize("n_heads,head_dim,rot_dim,base,scaling", [
+    (4, 5, 5, 10000.0, 1.0),         # odd head_dim: its last dimension is left alone, as in the reference
     (32, 128, 128, 500000.0, 1.0),   # Llama-3-8B q
     (8, 128, 128, 500000.0, 1.0),    # its k
     (9, 64, 64, 10000.0, 1.0),       # SmolLM
