@@ -48,7 +48,7 @@ struct DecodeParams {
     int pps;    // pages per split
     int max_splits;
     int max_len;  // host bound on kv_len: lengths are clamped to it, so splits never exceed max_splits
-    float q_mul;    // multiplier folded into q: scale*log2(e), or scale with a soft-cap
+    float q_mul;    // multiplier of q.k: scale*log2(e), or scale with a soft-cap
     float softcap;  // > 0: cap * tanh(s / cap)
 };
 
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
 #pragma unroll
         for (int i = 0; i < NCH; i++) {
 #pragma unroll
-            for (int e = 0; e < EPC; e++) qv[g][i * EPC + e] = qp[(i * 8 + sub) * EPC + e] * p.q_mul;
+            for (int e = 0; e < EPC; e++) qv[g][i * EPC + e] = qp[(i * 8 + sub) * EPC + e];
         }
     }
 
@@ -237,7 +237,9 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
             }
 #pragma unroll
             for (int g = 0; g < GT; g++) {
-                float x = sum8(dot[g]);
+                // q_mul on the score, not on q: q's loads then have no use
+                // before the K/V loads are issued, so their wait comes after
+                float x = sum8(dot[g]) * p.q_mul;
                 if (p.softcap > 0.0f) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
                 t[s][g] = x;
             }
@@ -493,13 +495,17 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
     // pages a window can span (a start inside a page adds one)
     const int max_pages = d.max_kv_len > 0 ? (d.max_kv_len + GLA_PAGE_SIZE - 1) / GLA_PAGE_SIZE + 1 : 1;
     const int64_t units = (int64_t)d.n_seqs * d.n_kv_heads * n_hg;
-    // Aim for about 8 workgroups per CU over the longest sequence; every wave
-    // of a split gets at least one iteration.
-    const int64_t target = 8LL * std::max(ctx->n_cu, 1);
-    int64_t splits_t = std::max<int64_t>(1, (target + units - 1) / units);
-    int pps = (int)std::max<int64_t>(1, (max_pages + splits_t - 1) / splits_t);
+    // About one workgroup per CU over the longest window (of max_kv_len
+    // positions; a start inside a page is left out of the sizing), at most
+    // 16 pages a split: at cfg2 (one sequence, 4,096 positions, 8 KV heads)
+    // 8-page splits measured 14.6 us per layer against 16.1 at 4 pages (twice
+    // the workgroups and partials), 16.4 at 16 and 22.7 at 32.
+    const int64_t target = std::max(ctx->n_cu, 1);
+    const int64_t splits_t = std::max<int64_t>(1, (target + units - 1) / units);
+    const int span = std::max(1, (d.max_kv_len + GLA_PAGE_SIZE - 1) / GLA_PAGE_SIZE);
+    int pps = (int)std::max<int64_t>(1, (span + splits_t - 1) / splits_t);
     const int quantum = kWaves * ppw;
-    pps = (pps + quantum - 1) / quantum * quantum;
+    pps = std::min((pps + quantum - 1) / quantum * quantum, std::max(16, quantum));
     if (const char *env = getenv("GLA_DECODE_PPS")) {
         int v = atoi(env);
         if (v > 0) pps = v;
