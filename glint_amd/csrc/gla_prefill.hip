@@ -528,6 +528,10 @@ __device__ __forceinline__ void store_tile_bf16(const TileBlocks<D, NTHR> &t, __
 template <int D>
 constexpr int kBf16Waves = D == 256 ? 4 : 8;
 
+// bf16 softmax: how far (log2 units) a score may pass the row's running
+// maximum before the maximum, and with it O, is rescaled.
+constexpr float kLazyMax = 8.0f;
+
 template <int D, bool Q8>
 __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const PrefillParams p) {
     constexpr int NW = kBf16Waves<D>, NT = 2, NTHR = NW * 64;
@@ -654,12 +658,17 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
                     }
                 }
                 mx = max_rows4(mx);
-                const float m_new = fmaxf(m[nt], mx);
+                // Lazy maximum: the row's reference moves only when a score
+                // passes it by more than 8 (log2 units), so p = 2^(s - m) stays
+                // at most 256 (exact range for bf16 and f32) and the rescale of
+                // O is rare; O / l is unchanged.
+                const bool up = mx > m[nt] + kLazyMax;
+                const float m_new = up ? mx : m[nt];
                 if (m_new == -INFINITY) {
                     pb[nt] = bf16x8{};
                     continue;
                 }
-                const float rs = fast_exp2(m[nt] - m_new);
+                const float rs = up ? fast_exp2(m[nt] - m_new) : 1.0f;
                 m[nt] = m_new;
                 float pr[2][4];
                 float ls = 0.0f;
@@ -964,12 +973,17 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
                     }
                 }
                 mx = max_rows4(mx);
-                const float m_new = fmaxf(m[nt], mx);
+                // Lazy maximum: the row's reference moves only when a score
+                // passes it by more than 8 (log2 units), so p = 2^(s - m) stays
+                // at most 256 (exact range for bf16 and f32) and the rescale of
+                // O is rare; O / l is unchanged.
+                const bool up = mx > m[nt] + kLazyMax;
+                const float m_new = up ? mx : m[nt];
                 if (m_new == -INFINITY) {
                     pb[nt] = bf16x8{};
                     continue;
                 }
-                const float rs = fast_exp2(m[nt] - m_new);
+                const float rs = up ? fast_exp2(m[nt] - m_new) : 1.0f;
                 m[nt] = m_new;
                 float pr[2][4];
                 float ls = 0.0f;
