@@ -676,10 +676,8 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
                 for (int mt = 0; mt < 2; mt++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        // the sum uses the bf16 value the MFMA multiplies
-                        const __bf16 h = (__bf16)fast_exp2(sacc[mt][nt][i] - m_new);
-                        pr[mt][i] = (float)h;
-                        ls += pr[mt][i];
+                        pr[mt][i] = fast_exp2(sacc[mt][nt][i] - m_new);
+                        ls += pr[mt][i];  // the f32 p; the MFMA takes it rounded to bf16
                     }
                 pb[nt] = bf16x8{(__bf16)pr[0][0], (__bf16)pr[0][1], (__bf16)pr[0][2], (__bf16)pr[0][3],
                                 (__bf16)pr[1][0], (__bf16)pr[1][1], (__bf16)pr[1][2], (__bf16)pr[1][3]};
@@ -991,10 +989,8 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
                 for (int mt = 0; mt < 2; mt++)
 #pragma unroll
                     for (int i2 = 0; i2 < 4; i2++) {
-                        // the sum uses the bf16 value the MFMA multiplies
-                        const __bf16 h = (__bf16)fast_exp2(sacc[mt][nt][i2] - m_new);
-                        pr[mt][i2] = (float)h;
-                        ls += pr[mt][i2];
+                        pr[mt][i2] = fast_exp2(sacc[mt][nt][i2] - m_new);
+                        ls += pr[mt][i2];  // the f32 p; the MFMA takes it rounded to bf16
                     }
                 pb[nt] = bf16x8{(__bf16)pr[0][0], (__bf16)pr[0][1], (__bf16)pr[0][2], (__bf16)pr[0][3],
                                 (__bf16)pr[1][0], (__bf16)pr[1][1], (__bf16)pr[1][2], (__bf16)pr[1][3]};
