@@ -66,20 +66,23 @@ __global__ __launch_bounds__(256) void mfma_bf16_kernel(int iters, float *sink) 
 
 template <typename F>
 int time_ms(F launch, int reps, float *ms_out) {
-    hipEvent_t e0, e1;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
     if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -2;
-    launch();  // warm-up
-    if (hipDeviceSynchronize() != hipSuccess) return -4;
-    hipEventRecord(e0, nullptr);
-    for (int i = 0; i < reps; i++) launch();
-    hipEventRecord(e1, nullptr);
-    if (hipEventSynchronize(e1) != hipSuccess) return -4;
     float ms = 0.0f;
-    hipEventElapsedTime(&ms, e0, e1);
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
+    int rc = 0;
+    launch();  // warm-up
+    if (hipDeviceSynchronize() != hipSuccess || hipEventRecord(e0, nullptr) != hipSuccess) {
+        rc = -4;
+    } else {
+        for (int i = 0; i < reps; i++) launch();
+        if (hipEventRecord(e1, nullptr) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+            hipEventElapsedTime(&ms, e0, e1) != hipSuccess || hipGetLastError() != hipSuccess)
+            rc = -4;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
     *ms_out = ms / reps;
-    return hipGetLastError() == hipSuccess ? 0 : -4;
+    return rc;
 }
 
 }  // namespace
@@ -91,7 +94,10 @@ int glp_stream_read(const void *buf, size_t bytes, int reps, double *gbs_out) {
     uint32_t *sink = nullptr;
     if (hipMalloc(&sink, 4) != hipSuccess) return -3;
     int n_cu = 0;
-    hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, 0);
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess || n_cu <= 0) {
+        (void)hipFree(sink);
+        return -3;
+    }
     const size_t n = bytes / 16;
     float ms = 0.0f;
     const int rc = time_ms(
@@ -100,7 +106,7 @@ int glp_stream_read(const void *buf, size_t bytes, int reps, double *gbs_out) {
                                static_cast<const u32x4 *>(buf), n, sink);
         },
         reps, &ms);
-    hipFree(sink);
+    (void)hipFree(sink);
     if (rc != 0) return rc;
     *gbs_out = (double)bytes / (ms * 1e-3) / 1e9;
     return 0;
@@ -112,7 +118,10 @@ int glp_mfma_peak(int kind, int iters, double *tflops_out) {
     float *sink = nullptr;
     if (hipMalloc(&sink, 4) != hipSuccess) return -3;
     int n_cu = 0;
-    hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, 0);
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess || n_cu <= 0) {
+        (void)hipFree(sink);
+        return -3;
+    }
     const dim3 grid(n_cu * 2), block(256);
     float ms = 0.0f;
     int rc;
@@ -124,7 +133,7 @@ int glp_mfma_peak(int kind, int iters, double *tflops_out) {
         rc = time_ms([&] { hipLaunchKernelGGL(mfma_bf16_kernel, grid, block, 0, nullptr, iters, sink); }, 3, &ms);
         flops_per_mfma = 16.0 * 16 * 32 * 2;
     }
-    hipFree(sink);
+    (void)hipFree(sink);
     if (rc != 0) return rc;
     const double waves = (double)grid.x * 4;
     *tflops_out = waves * iters * 8 * flops_per_mfma / (ms * 1e-3) / 1e12;
