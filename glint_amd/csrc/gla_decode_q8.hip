@@ -890,17 +890,19 @@ int host_seq_pages(int start, int len, int max_len, int pos_limit) {
     return e > s ? (int)(((e - 1) >> 4) - (s >> 4) + 1) : 0;
 }
 
-// Pages per chunk: 20 (10 steps), measured best on the Llama-3-8B and
-// Gemma-2-9B batch decodes (chunk sizes 12..52 span ~20%: shorter chunks
-// repeat the q / page-id / V-scale set-up more often, longer ones leave the
-// grid's last workgroups running alone). A batch too small to give every
-// resident workgroup slot a workgroup at 20 gets shorter chunks, down to 2.
+// Pages per chunk: 28 (14 steps), measured best on the Llama-3-8B and
+// Gemma-2-9B batch decodes with the workgroups dispatched longest first
+// (shorter chunks repeat the q / page-id / V-scale set-up more often, longer
+// ones leave the grid's last workgroups running alone; 20 was best before the
+// longest-first order, which takes most of that tail away). A batch too small
+// to give every resident workgroup slot a workgroup at 28 gets shorter
+// chunks, down to 2.
 // With the pages of every sequence known (np) the counts are exact; without
 // them every sequence is taken to span max_pages.
 int choose_chunk_pages(const std::vector<int> &np, int n_seqs, int max_pages, int n_hu, int64_t slots) {
     // at most 64 pages per wave (one page id per lane), even past kMaxChunks chunks
     const int lo = std::min(64, std::max(2, (max_pages + kMaxChunks - 1) / kMaxChunks));
-    int ch = std::min(64, std::max(20, (lo + 1) & ~1));
+    int ch = std::min(64, std::max(28, (lo + 1) & ~1));
     for (; ch > 2 && ch - 2 >= lo; ch -= 2) {
         int64_t wgs = 0;
         if (np.empty()) {
