@@ -890,19 +890,19 @@ int host_seq_pages(int start, int len, int max_len, int pos_limit) {
     return e > s ? (int)(((e - 1) >> 4) - (s >> 4) + 1) : 0;
 }
 
-// Pages per chunk: 28 (14 steps), measured best on the Llama-3-8B and
-// Gemma-2-9B batch decodes with the workgroups dispatched longest first
-// (shorter chunks repeat the q / page-id / V-scale set-up more often, longer
-// ones leave the grid's last workgroups running alone; 20 was best before the
-// longest-first order, which takes most of that tail away). A batch too small
-// to give every resident workgroup slot a workgroup at 28 gets shorter
-// chunks, down to 2.
+// Pages per chunk: 28 (14 steps) for head_dim up to 128, 40 for 256,
+// measured best on the Llama-3-8B and Gemma-2-9B batch decodes with the
+// workgroups dispatched longest first (shorter chunks repeat the q / page-id
+// / V-scale set-up more often, longer ones leave the grid's last workgroups
+// running alone; 20 was best before the longest-first order, which takes
+// most of that tail away). A batch too small to give every resident
+// workgroup slot a workgroup at that size gets shorter chunks, down to 2.
 // With the pages of every sequence known (np) the counts are exact; without
 // them every sequence is taken to span max_pages.
-int choose_chunk_pages(const std::vector<int> &np, int n_seqs, int max_pages, int n_hu, int64_t slots) {
+int choose_chunk_pages(const std::vector<int> &np, int n_seqs, int max_pages, int n_hu, int64_t slots, int D) {
     // at most 64 pages per wave (one page id per lane), even past kMaxChunks chunks
     const int lo = std::min(64, std::max(2, (max_pages + kMaxChunks - 1) / kMaxChunks));
-    int ch = std::min(64, std::max(28, (lo + 1) & ~1));
+    int ch = std::min(64, std::max(D == 256 ? 40 : 28, (lo + 1) & ~1));
     for (; ch > 2 && ch - 2 >= lo; ch -= 2) {
         int64_t wgs = 0;
         if (np.empty()) {
@@ -934,7 +934,7 @@ int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
     }
     int per_cu = D == 64 ? resident_wgs<64>() : (D == 128 ? resident_wgs<128>() : resident_wgs<256>());
     const int64_t slots = (int64_t)std::max(ctx->n_cu, 1) * std::max(per_cu, 1);
-    int64_t ch = choose_chunk_pages(np, d.n_seqs, (int)max_pages, d.n_kv_heads * n_hg, slots);
+    int64_t ch = choose_chunk_pages(np, d.n_seqs, (int)max_pages, d.n_kv_heads * n_hg, slots, D);
     if (const char *env = getenv("GLA_Q8_CHUNK_PAGES")) {
         const int v = atoi(env);
         if (v > 0) ch = std::min(64, (v + 1) & ~1);
