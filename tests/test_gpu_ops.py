@@ -116,3 +116,30 @@ def test_matvec_q8_0_matches_oracle_and_f64(backend, rows, cols, n_vec):
     for v in (0, n_vec // 2, n_vec - 1):
         want = orc.matvec_q8_0(raw, rows, cols, x[v])
         assert np.all(np.abs(got[v] - want) <= 4e-6 * mag[v]), v
+
+
+def test_ops_argument_errors_and_empty_calls(backend):
+    """Shapes the ABI rejects come back as GLA_ERR_INVALID (the caller's CPU path), and empty
+    calls are no-ops: zero vectors, zero rows, a rotary dimension of 0 or 1 (no whole pair)."""
+    from glint_amd._lib import GLA_ERR_INVALID, GlaError
+
+    raw = _q8_rows(16, 64, 7)
+    with pytest.raises(GlaError) as e:
+        backend.create_q8_weights(np.zeros(34 * 3, np.uint8), 1, 96 + 16)  # cols not a multiple of 32
+    assert e.value.code == GLA_ERR_INVALID
+    w = backend.create_q8_weights(raw, 16, 64)
+    y = backend.buffer(np.full(16, 7.0, np.float32))
+    backend.matvec_q8_0(w, backend.empty(64 * 4), 0, y)  # no vectors: y untouched
+    backend.sync()
+    assert np.all(y.download((16,)) == 7.0)
+    with pytest.raises(GlaError) as e:
+        backend.matvec_q8_0(w, backend.empty(64 * 4), -1, y)
+    assert e.value.code == GLA_ERR_INVALID
+    w.destroy()
+
+    x = synth.normal(3, (2, 2, 8))
+    for rot in (0, 1):  # no whole pair below rot: nothing moves
+        assert np.array_equal(_rope_gpu(backend, x, [5, 9], 8, 10000.0, 1.0, rot), x)
+    with pytest.raises(GlaError) as e:
+        _rope_gpu(backend, x, [5, 9], 0, 10000.0, 1.0, 8)  # head_dim 0
+    assert e.value.code == GLA_ERR_INVALID
