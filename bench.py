@@ -527,6 +527,16 @@ def main() -> int:
         if not args.no_cpu:
             secondary["cfg1"]["cpu_baseline"] = wl.cpu_baseline(min_seconds=2.0, max_reps=20000)
         log(f"cfg1: {ms * 1e3:.2f} us/call")
+        # the same layers' calls captured as one HIP graph (a decode step's attention), replayed:
+        # the launch cost of a call is then paid once per step, not once per kernel
+        g = be.capture(lambda: [wl.step(i) for i in range(wl.n_layers)])
+        ms_g = time_steps(be, ev, lambda i: g.replay(), max(args.steps, 64), args.warmup) / wl.n_layers
+        g.destroy()
+        secondary["cfg1_graph"] = {
+            "workload": f"cfg1, the {wl.n_layers} layers' gla_decode calls captured as one HIP graph and replayed",
+            "value": round(ms_g * 1e3, 2), "unit": "us/call",
+            "GB_per_s": round(wl.bytes_per_step() / (ms_g * 1e-3) / 1e9, 2)}
+        log(f"cfg1 graph: {ms_g * 1e3:.2f} us/call")
         del wl
     if "cfg4" in want:
         log("cfg4: 4x2048 causal prefill, f32 KV cache")

@@ -222,6 +222,69 @@ class Q8Weights:
             pass
 
 
+_HIP = None
+
+
+def _hip() -> C.CDLL:
+    """The HIP runtime the library is linked against (already loaded with it)."""
+    global _HIP
+    if _HIP is None:
+        _lib.lib()
+        for name in ("libamdhip64.so", "/opt/rocm/lib/libamdhip64.so"):
+            try:
+                _HIP = C.CDLL(name)
+                break
+            except OSError:
+                continue
+        if _HIP is None:
+            raise GlaError(_lib.GLA_ERR_DEVICE, "libamdhip64.so not found")
+        for fn, args in (("hipStreamBeginCapture", [C.c_void_p, C.c_int]),
+                         ("hipStreamEndCapture", [C.c_void_p, C.POINTER(C.c_void_p)]),
+                         ("hipGraphInstantiate", [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p,
+                                                  C.c_size_t]),
+                         ("hipGraphLaunch", [C.c_void_p, C.c_void_p]),
+                         ("hipGraphExecDestroy", [C.c_void_p]),
+                         ("hipGraphDestroy", [C.c_void_p])):
+            f = getattr(_HIP, fn)
+            f.argtypes, f.restype = args, C.c_int
+    return _HIP
+
+
+def _hip_check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise GlaError(_lib.GLA_ERR_DEVICE, f"{what}: hipError {rc}")
+
+
+class HipGraph:
+    """Library calls captured on a backend's stream and replayed with one hipGraphLaunch.
+    A replay repeats the captured launches exactly: the same buffers (whose contents may
+    change between replays), shapes and host-side launch decisions -- and the same context
+    scratch. A call on the backend that needs more scratch than any captured call reallocates
+    it and leaves the graph pointing at freed memory: size the scratch first (run the largest
+    calls before capturing), or capture on a GpuBackend of its own."""
+
+    def __init__(self, backend: "GpuBackend", graph: C.c_void_p, exe: C.c_void_p):
+        self.backend, self.graph, self.exe = backend, graph, exe
+
+    def replay(self) -> None:
+        """Enqueue the graph on the backend's stream (asynchronous, like the calls it holds)."""
+        _hip_check(_hip().hipGraphLaunch(self.exe, C.c_void_p(self.backend.stream)), "hipGraphLaunch")
+
+    def destroy(self) -> None:
+        if self.exe:
+            _hip().hipGraphExecDestroy(self.exe)
+            self.exe = None
+        if self.graph:
+            _hip().hipGraphDestroy(self.graph)
+            self.graph = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
 class GpuBackend:
     """One HIP device and stream (gla_ctx). Mirrors GpuBackend::new's failure mode:
     no device -> GlaError named GpuAdapterNotFound, and the caller keeps its CPU path."""
@@ -253,6 +316,26 @@ class GpuBackend:
     @property
     def cu_count(self) -> int:
         return int(_lib.lib().gla_device_cu_count(self.ctx))
+
+    def capture(self, calls) -> HipGraph:
+        """Capture ``calls()`` -- device-pointer library calls on this backend, e.g. a decode
+        step's layers -- into a HIP graph. Run the same calls once beforehand, so that no call
+        grows its scratch (allocates) during the capture."""
+        hip = _hip()
+        stream = C.c_void_p(self.stream)
+        _hip_check(hip.hipStreamBeginCapture(stream, 1), "hipStreamBeginCapture")  # thread-local mode
+        graph = C.c_void_p()
+        try:
+            calls()
+        finally:
+            rc = hip.hipStreamEndCapture(stream, C.byref(graph))
+        _hip_check(rc, "hipStreamEndCapture")
+        exe = C.c_void_p()
+        rc = hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0)
+        if rc != 0:
+            hip.hipGraphDestroy(graph)
+            _hip_check(rc, "hipGraphInstantiate")
+        return HipGraph(self, graph, exe)
 
     def buffer(self, a: np.ndarray) -> DeviceBuffer:
         return DeviceBuffer.from_numpy(self, a)

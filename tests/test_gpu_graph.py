@@ -1,0 +1,72 @@
+"""HIP graph capture of library calls (GpuBackend.capture): a decode step's calls -- a paged
+Q8_0 batch decode, three layers of a contiguous f32 decode, a Q8_0 projection and RoPE on its
+output -- captured once and replayed. Between replays new inputs are uploaded and the same calls
+run eagerly into other buffers; every replay equals the eager calls bit for bit (the kernels are
+deterministic, and the graph must read the buffers' current contents)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from glint_amd import synth
+from gpu_util import Contig, Pool
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_replays_equal_eager_calls(backend):
+    be = backend
+    # paged Q8_0 decode: 4 sequences, Llama-3 head shape, soft-capped
+    H, Hkv, d = 8, 2, 128
+    pb = synth.paged_batch(11, np.array([5, 40, 300, 129], np.int32), prefix_tokens=32)
+    p = Pool(be, "q8", pb, Hkv, d, seed=12)
+    ds, dl, dt = be.buffer(pb.kv_start), be.buffer(pb.kv_len), be.buffer(pb.table)
+    # contiguous f32 decode: one sequence, 3 layers, SmolLM head shape, ctx 512
+    c = Contig(be, "f32", 1, 3, 512, 3, 64, seed=13)
+    dsf, dlf = be.buffer(np.array([0], np.int32)), be.buffer(np.array([512], np.int32))
+    # a 48 x 96 Q8_0 projection of 2 tokens, then RoPE on its rows (3 heads of 16)
+    raw = orc.q8_quantize_rows(synth.normal_rows(14, 48, 96)).reshape(-1)
+    w = be.create_q8_weights(raw, 48, 96)
+    dpos = be.buffer(np.array([7, 300], np.int32))
+
+    dq8, dqf, dx = be.empty(4 * H * d * 4), be.empty(9 * 64 * 4), be.empty(2 * 96 * 4)
+    o8 = [be.empty(4 * H * d * 4) for _ in range(2)]      # [eager, graph]
+    of = [[be.empty(9 * 64 * 4) for _ in range(3)] for _ in range(2)]
+    oy = [be.empty(2 * 48 * 4) for _ in range(2)]
+
+    def calls(k):
+        be.decode(p.pool, dq8, o8[k], ds, dl, 4, int(pb.kv_len.max()), H, 0.088, 30.0,
+                  page_table=dt, page_table_stride=pb.table.shape[1], kv_start_host=pb.kv_start,
+                  kv_len_host=pb.kv_len)
+        for layer in range(3):
+            be.decode(c.cache, dqf, of[k][layer], dsf, dlf, 1, 512, 9, 0.125, layer=layer)
+        be.matvec_q8_0(w, dx, 2, oy[k])
+        be.rope(oy[k], 2, 3, 16, dpos, 10000.0, 1.0, 16)
+
+    rng = np.random.default_rng(15)
+
+    def new_inputs():
+        dq8.upload(rng.standard_normal(4 * H * d).astype(np.float32))
+        dqf.upload(rng.standard_normal(9 * 64).astype(np.float32))
+        dx.upload(rng.standard_normal(2 * 96).astype(np.float32))
+
+    new_inputs()
+    calls(0)  # sizes the scratch: nothing allocates during the capture
+    be.sync()
+    g = be.capture(lambda: calls(1))
+    try:
+        for rep in range(4):
+            new_inputs()
+            calls(0)
+            g.replay()
+            be.sync()
+            pairs = [(o8[0], o8[1], 4 * H * d), (oy[0], oy[1], 96)]
+            pairs += [(of[0][layer], of[1][layer], 9 * 64) for layer in range(3)]
+            for a, b, n in pairs:
+                ea, eb = a.download((n,)), b.download((n,))
+                assert np.isfinite(ea).all()
+                assert np.array_equal(ea.view(np.uint32), eb.view(np.uint32)), rep
+    finally:
+        g.destroy()
+        w.destroy()
