@@ -7,9 +7,10 @@ Prints ONE JSON line. `value` is BASELINE's headline metric on its headline
 workload: achieved HBM GB/s of Llama-3-8B-shaped paged Q8_0 decode attention
 at batch 64 (config 3), with every input resident in HBM. The other
 configurations are reported under "secondary": config 1 (SmolLM decode
-latency), config 2 (32 layers of f32 decode), config 4 (4x2048 causal
-prefill, TFLOP/s), config 5 (Gemma-2 windowed + global decode) and "proj",
-the Q8_0 QKV projection matvec beside attention (1 and 64 tokens).
+latency, eagerly and with its layers' calls replayed as one HIP graph),
+config 2 (32 layers of f32 decode), config 4 (4x2048 causal prefill,
+TFLOP/s), config 5 (Gemma-2 windowed + global decode) and "proj", the Q8_0
+QKV projection matvec beside attention (1 and 64 tokens).
 
 A step is one gla_decode (or gla_prefill) call over the whole batch for one
 layer. W untimed steps, then K steps between two HIP events recorded on the
