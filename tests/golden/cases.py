@@ -145,6 +145,46 @@ def q8_codec_rows() -> np.ndarray:
     return x
 
 
+@dataclass
+class OpsCase:
+    """The ops beside attention: RoPE over rows of heads (src/tensor/ops.rs:212-245) and a
+    Q8_0 matvec (src/tensor/quantized.rs:587-610)."""
+    name: str
+    kind: str  # "rope" or "matvec"
+    x: np.ndarray
+    pos: Optional[np.ndarray] = None  # rope: one position per row
+    head_dim: int = 0
+    rot_dim: int = 0
+    base: float = 0.0
+    scaling: float = 1.0
+    raw: Optional[np.ndarray] = None  # matvec: GGML Q8_0 bytes [rows][cols/32 x 34]
+    rows: int = 0
+    cols: int = 0
+    inputs: List[np.ndarray] = field(default_factory=list)
+
+
+def ops_rope() -> OpsCase:
+    """Partial rotary (24 of 32 dimensions) with linear scaling 2, positions up to 65,535."""
+    x = synth.normal(0x0B01, (4, 3, 32))
+    pos = np.array([0, 17, 4095, 65535], np.int32)
+    c = OpsCase("ops_rope", "rope", x, pos=pos, head_dim=32, rot_dim=24, base=500000.0, scaling=2.0)
+    c.inputs = [x, pos]
+    return c
+
+
+def ops_matvec_q8_0() -> OpsCase:
+    """A 70 x 160 Q8_0 matrix (5 blocks per row: an odd block count, and a row tile of 6) times
+    5 vectors (the vector-ALU path's limit is 4: this takes the MFMA path)."""
+    import oracle as orc
+
+    w = synth.normal_rows(0x0B02, 70, 160)
+    raw = orc.q8_quantize_rows(w).reshape(-1)
+    x = synth.normal(0x0B03, (5, 160))
+    c = OpsCase("ops_matvec_q8_0", "matvec", x, raw=raw, rows=70, cols=160)
+    c.inputs = [raw, x]
+    return c
+
+
 DECODE_CASES: Dict[str, Callable[[], DecodeCase]] = {
     "decode_cfg1": decode_cfg1,
     "decode_q8_paged": decode_q8_paged,
@@ -152,6 +192,10 @@ DECODE_CASES: Dict[str, Callable[[], DecodeCase]] = {
 }
 PREFILL_CASES: Dict[str, Callable[[], PrefillCase]] = {
     "prefill_varlen": prefill_varlen,
+}
+OPS_CASES: Dict[str, Callable[[], OpsCase]] = {
+    "ops_rope": ops_rope,
+    "ops_matvec_q8_0": ops_matvec_q8_0,
 }
 
 
@@ -189,3 +233,12 @@ def oracle_prefill(c: PrefillCase) -> np.ndarray:
         out[r0:r1] = orc.prefill(c.q[r0:r1].reshape(r1 - r0, -1), st, 0, int(c.pos_offset[b]), c.H, c.Hkv, c.d,
                                  c.scale, c.softcap, c.window).reshape(r1 - r0, c.H, c.d)
     return out
+
+
+def oracle_ops(c: OpsCase) -> np.ndarray:
+    import oracle as orc
+
+    if c.kind == "rope":
+        return np.stack([orc.rope(c.x[r].reshape(-1), int(c.pos[r]), c.head_dim, c.base, c.scaling,
+                                  c.rot_dim).reshape(c.x.shape[1:]) for r in range(c.x.shape[0])]).astype(np.float32)
+    return np.stack([orc.matvec_q8_0(c.raw, c.rows, c.cols, c.x[v]) for v in range(c.x.shape[0])]).astype(np.float32)

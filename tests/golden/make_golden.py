@@ -36,6 +36,11 @@ def main() -> None:
         np.savez_compressed(HERE / f"{name}.npz", out=cases.oracle_prefill(c),
                             inputs_sha256=np.array(cases.digest(c.inputs)))
         print("wrote", name)
+    for name, make in cases.OPS_CASES.items():
+        c = make()
+        np.savez_compressed(HERE / f"{name}.npz", out=cases.oracle_ops(c),
+                            inputs_sha256=np.array(cases.digest(c.inputs)))
+        print("wrote", name)
     x = cases.q8_codec_rows()
     np.savez_compressed(HERE / "q8_codec.npz", bytes=orc.q8_quantize_rows(x),
                         inputs_sha256=np.array(cases.digest([x])))

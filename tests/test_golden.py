@@ -45,6 +45,14 @@ def test_prefill_fixture_oracle(name):
     assert np.array_equal(cases.oracle_prefill(c).view(np.uint32), fx["out"].view(np.uint32))
 
 
+@pytest.mark.parametrize("name", list(cases.OPS_CASES))
+def test_ops_fixture_oracle(name):
+    c = cases.OPS_CASES[name]()
+    fx = _fixture(name)
+    assert cases.digest(c.inputs) == str(fx["inputs_sha256"]), "input generator changed"
+    assert np.array_equal(cases.oracle_ops(c).view(np.uint32), fx["out"].view(np.uint32))
+
+
 def test_q8_codec_fixture_oracle():
     x = cases.q8_codec_rows()
     fx = _fixture("q8_codec")
@@ -89,3 +97,32 @@ def test_q8_codec_fixture_gpu(backend):
     pool.write_rows(rows, x, x)
     kb, vb = pool.export_rows(rows)
     assert np.array_equal(kb, want) and np.array_equal(vb, want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", list(cases.OPS_CASES))
+def test_ops_fixture_gpu(backend, name):
+    """RoPE within 1e-5 x max|x| (the angles match the reference's; cos/sin may differ in the
+    last place); the matvec within 4e-6 x sum |w x| per output of the oracle's f32 sums (both
+    sides' rounding, as tests/test_gpu_ops.py bounds it against the oracle)."""
+    c = cases.OPS_CASES[name]()
+    want = _fixture(name)["out"]
+    if c.kind == "rope":
+        dx = backend.buffer(np.ascontiguousarray(c.x, np.float32))
+        backend.rope(dx, c.x.shape[0], c.x.shape[1], c.head_dim, backend.buffer(c.pos), c.base, c.scaling,
+                     c.rot_dim)
+        backend.sync()
+        got = dx.download(c.x.shape)
+        assert np.abs(got - want).max() <= 1e-5 * np.abs(c.x).max()
+        return
+    w = backend.create_q8_weights(c.raw, c.rows, c.cols)
+    dy = backend.empty(c.x.shape[0] * c.rows * 4)
+    backend.matvec_q8_0(w, backend.buffer(c.x), c.x.shape[0], dy)
+    backend.sync()
+    got = dy.download((c.x.shape[0], c.rows))
+    w.destroy()
+    blk = c.raw.reshape(c.rows, c.cols // 32, 34)
+    scale = blk[:, :, :2].copy().view(np.float16).astype(np.float64)
+    wd = (blk[:, :, 2:].view(np.int8).astype(np.float64) * scale).reshape(c.rows, c.cols)
+    mag = np.abs(c.x.astype(np.float64)) @ np.abs(wd).T
+    assert np.all(np.abs(got - want) <= 4e-6 * mag)
