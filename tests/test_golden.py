@@ -4,8 +4,9 @@ CPU: every case's seeded inputs still hash to the recorded SHA-256, and the
 oracle still reproduces the stored output bit for bit (a regression pin on the
 oracle and on the input generator).
 GPU: the kernels, through the C ABI, match the stored outputs at the fp32 bar
-(max abs 1e-4 / rel 1e-3); the Q8_0 bytes written on the device equal the
-stored Glint-format bytes exactly.
+(max abs 1e-4 / rel 1e-3; the ops at their own bars, stated in their test);
+the Q8_0 bytes written on the device equal the stored Glint-format bytes
+exactly.
 """
 from __future__ import annotations
 
