@@ -320,7 +320,9 @@ class GpuBackend:
     def capture(self, calls) -> HipGraph:
         """Capture ``calls()`` -- device-pointer library calls on this backend, e.g. a decode
         step's layers -- into a HIP graph. Run the same calls once beforehand, so that no call
-        grows its scratch (allocates) during the capture."""
+        grows its scratch (allocates) during the capture. A later call that needs more scratch
+        moves to a new buffer and leaves the old one allocated until the context is destroyed,
+        so the graph's pointers stay valid."""
         hip = _hip()
         stream = C.c_void_p(self.stream)
         _hip_check(hip.hipStreamBeginCapture(stream, 1), "hipStreamBeginCapture")  # thread-local mode

@@ -50,35 +50,30 @@ KvLayout layout_of(const gla_kv *kv) {
     return L;
 }
 
-static int grow(void **ptr, size_t *cur, size_t need, hipStream_t stream, bool pinned) {
+// Grow *ptr to at least `need` bytes (doubling). The old buffer is retired,
+// not freed: kernels still queued on the stream and graphs captured from it
+// keep their pointers, so growing needs no synchronisation.
+static int grow(gla_ctx *ctx, void **ptr, size_t *cur, size_t need, bool pinned) {
     if (need <= *cur) return GLA_OK;
     size_t want = std::max(need, *cur * 2);
-    if (*ptr) {
-        GLA_CHECK_HIP(hipStreamSynchronize(stream), GLA_ERR_DEVICE);
-        if (pinned)
-            (void)hipHostFree(*ptr);
-        else
-            (void)hipFree(*ptr);
-        *ptr = nullptr;
-        *cur = 0;
-    }
-    hipError_t e = pinned ? hipHostMalloc(ptr, want, hipHostMallocDefault) : hipMalloc(ptr, want);
-    if (e != hipSuccess) {
-        *ptr = nullptr;
+    void *fresh = nullptr;
+    hipError_t e = pinned ? hipHostMalloc(&fresh, want, hipHostMallocDefault) : hipMalloc(&fresh, want);
+    if (e != hipSuccess)
         return set_error(GLA_ERR_BUFFER, "allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
-    }
+    if (*ptr) ctx->retired.emplace_back(*ptr, pinned);
+    *ptr = fresh;
     *cur = want;
     return GLA_OK;
 }
 
 int ensure_scratch(gla_ctx *ctx, size_t bytes) {
-    return grow(&ctx->scratch, &ctx->scratch_bytes, bytes, ctx->stream, false);
+    return grow(ctx, &ctx->scratch, &ctx->scratch_bytes, bytes, false);
 }
 int ensure_dstage(gla_ctx *ctx, size_t bytes) {
-    return grow(&ctx->dstage, &ctx->dstage_bytes, bytes, ctx->stream, false);
+    return grow(ctx, &ctx->dstage, &ctx->dstage_bytes, bytes, false);
 }
 int ensure_hstage(gla_ctx *ctx, size_t bytes) {
-    return grow(&ctx->hstage, &ctx->hstage_bytes, bytes, ctx->stream, true);
+    return grow(ctx, &ctx->hstage, &ctx->hstage_bytes, bytes, true);
 }
 
 static bool head_dim_ok(int d) { return d == 64 || d == 128 || d == 256; }
@@ -146,6 +141,12 @@ int gla_destroy(gla_ctx *ctx) {
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->dstage) (void)hipFree(ctx->dstage);
     if (ctx->hstage) (void)hipHostFree(ctx->hstage);
+    for (const auto &r : ctx->retired) {
+        if (r.second)
+            (void)hipHostFree(r.first);
+        else
+            (void)hipFree(r.first);
+    }
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return GLA_OK;

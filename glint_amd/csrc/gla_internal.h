@@ -36,6 +36,8 @@
 #include <stdint.h>
 
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/glint_attn.h"
 
@@ -125,6 +127,10 @@ struct gla_ctx {
     size_t dstage_bytes = 0;
     void *hstage = nullptr;
     size_t hstage_bytes = 0;
+    // Buffers replaced by a larger one, kept until gla_destroy: work already
+    // queued, and any HIP graph captured from the stream, still address them
+    // (second: pinned host memory).
+    std::vector<std::pair<void *, bool>> retired;
 };
 
 struct gla_kv {

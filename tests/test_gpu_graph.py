@@ -2,7 +2,9 @@
 Q8_0 batch decode, three layers of a contiguous f32 decode, a Q8_0 projection and RoPE on its
 output -- captured once and replayed. Between replays new inputs are uploaded and the same calls
 run eagerly into other buffers; every replay equals the eager calls bit for bit (the kernels are
-deterministic, and the graph must read the buffers' current contents)."""
+deterministic, and the graph must read the buffers' current contents). Before the last replays an
+eager call with a much larger scratch need (a 64-token projection of 4096 columns) makes the
+context allocate a larger scratch; the graph keeps the old buffer, which stays allocated."""
 from __future__ import annotations
 
 import numpy as np
@@ -55,8 +57,14 @@ def test_graph_replays_equal_eager_calls(backend):
     calls(0)  # sizes the scratch: nothing allocates during the capture
     be.sync()
     g = be.capture(lambda: calls(1))
+    big = be.create_q8_weights(orc.q8_quantize_rows(synth.normal_rows(16, 512, 4096)).reshape(-1), 512, 4096)
     try:
-        for rep in range(4):
+        for rep in range(6):
+            if rep == 4:  # grow the scratch after the capture: ~2 MiB of pieces and partials
+                bx, by = be.buffer(rng.standard_normal(64 * 4096).astype(np.float32)), be.empty(64 * 512 * 4)
+                be.matvec_q8_0(big, bx, 64, by)
+                be.sync()
+                assert np.isfinite(by.download((64 * 512,))).all()
             new_inputs()
             calls(0)
             g.replay()
@@ -70,3 +78,4 @@ def test_graph_replays_equal_eager_calls(backend):
     finally:
         g.destroy()
         w.destroy()
+        big.destroy()
