@@ -69,6 +69,32 @@ __device__ __forceinline__ float tanh_approx(float x) {
     return copysignf(r, x);
 }
 
+// Soft-cap and causal/window mask of one query column of a 32-key score tile
+// (sacc[mt][i]: key k0 + 16*mt + 4*lgrp + i), in place, log2 domain. The
+// soft-cap is a template argument and the mask one wave-uniform branch per
+// tile with selects inside: written per score, both conditions became a
+// branch around every score.
+template <bool CAP>
+__device__ __forceinline__ void cap_and_mask(floatx4 (&s)[2], float softcap, bool interior, int kbase, int qpos,
+                                             int qlo, int klo, int khi) {
+    if constexpr (CAP) {
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[mt][i] = softcap * tanh_approx(s[mt][i] / softcap) * kLog2e;
+    }
+    if (!interior) {
+        const int lo = max(qlo, klo), hi = min(qpos, khi);
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int kp = kbase + mt * 16 + i;
+                s[mt][i] = (kp >= lo && kp <= hi) ? s[mt][i] : -INFINITY;
+            }
+    }
+}
+
 __device__ __forceinline__ int window_lo(int pos, int w) {
     if (w <= 0) return 0;
     int s = pos - w + 1;
@@ -181,7 +207,7 @@ __device__ __forceinline__ void store_tile(const TileRegs<D, NTHR> &t, float *Ks
 // O^T row R of d-tile t is d = R*DT + t, so the V^T operands a lane needs
 // for one key are DT consecutive floats, and a lane's outputs for a query
 // are the 4*DT consecutive floats [4g*DT, 4(g+1)*DT).
-template <int D, int NT, int NW, bool Q8>
+template <int D, int NT, int NW, bool Q8, bool CAP>
 __global__ __launch_bounds__(NW * 64) void prefill_f32_kernel(const PrefillParams p) {
     constexpr int NTHR = NW * 64;
     constexpr int QW = 16 * NT;  // queries per wave
@@ -303,22 +329,15 @@ __global__ __launch_bounds__(NW * 64) void prefill_f32_kernel(const PrefillParam
                                   (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
+                floatx4 col[2] = {sacc[0][nt], sacc[1][nt]};
+                cap_and_mask<CAP>(col, p.softcap, interior, k0 + 4 * lgrp, qpos[nt], qlo[nt], klo, khi);
+                sacc[0][nt] = col[0];
+                sacc[1][nt] = col[1];
                 float mx = -INFINITY;
 #pragma unroll
-                for (int mt = 0; mt < 2; mt++) {
+                for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int kp = k0 + mt * 16 + 4 * lgrp + i;
-                        float x = sacc[mt][nt][i];
-                        if (p.softcap > 0.0f) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
-                        if (!interior) {
-                            const bool ok = kp <= qpos[nt] && kp >= qlo[nt] && kp >= klo && kp <= khi;
-                            x = ok ? x : -INFINITY;
-                        }
-                        sacc[mt][nt][i] = x;
-                        mx = fmaxf(mx, x);
-                    }
-                }
+                    for (int i = 0; i < 4; i++) mx = fmaxf(mx, sacc[mt][nt][i]);
                 mx = max_rows4(mx);
                 const float m_new = fmaxf(m[nt], mx);
                 if (m_new == -INFINITY) {
@@ -532,7 +551,7 @@ constexpr int kBf16Waves = D == 256 ? 4 : 8;
 // maximum before the maximum, and with it O, is rescaled.
 constexpr float kLazyMax = 8.0f;
 
-template <int D, bool Q8>
+template <int D, bool Q8, bool CAP>
 __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const PrefillParams p) {
     constexpr int NW = kBf16Waves<D>, NT = 2, NTHR = NW * 64;
     constexpr int QW = 16 * NT;
@@ -641,22 +660,15 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
             bf16x8 pb[NT];
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
+                floatx4 col[2] = {sacc[0][nt], sacc[1][nt]};
+                cap_and_mask<CAP>(col, p.softcap, interior, k0 + 4 * lgrp, qpos[nt], qlo[nt], klo, khi);
+                sacc[0][nt] = col[0];
+                sacc[1][nt] = col[1];
                 float mx = -INFINITY;
 #pragma unroll
-                for (int mt = 0; mt < 2; mt++) {
+                for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int kp = k0 + mt * 16 + 4 * lgrp + i;
-                        float x = sacc[mt][nt][i];
-                        if (p.softcap > 0.0f) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
-                        if (!interior) {
-                            const bool ok = kp <= qpos[nt] && kp >= qlo[nt] && kp >= klo && kp <= khi;
-                            x = ok ? x : -INFINITY;
-                        }
-                        sacc[mt][nt][i] = x;
-                        mx = fmaxf(mx, x);
-                    }
-                }
+                    for (int i = 0; i < 4; i++) mx = fmaxf(mx, sacc[mt][nt][i]);
                 mx = max_rows4(mx);
                 // Lazy maximum: the row's reference moves only when a score
                 // passes it by more than 8 (log2 units), so p = 2^(s - m) stays
@@ -832,7 +844,7 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
 template <int D>
 constexpr int kBf16sWaves = D == 64 ? 16 : (D == 128 ? 12 : 4);
 
-template <int D>
+template <int D, bool CAP>
 __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(const PrefillParams p,
                                                                           const uint8_t *img, int n_tiles) {
     constexpr int NW = kBf16sWaves<D>, NT = 2;
@@ -954,22 +966,15 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
             bf16x8 pb[NT];
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
+                floatx4 col[2] = {sacc[0][nt], sacc[1][nt]};
+                cap_and_mask<CAP>(col, p.softcap, interior, k0 + 4 * lgrp, qpos[nt], qlo[nt], klo, khi);
+                sacc[0][nt] = col[0];
+                sacc[1][nt] = col[1];
                 float mx = -INFINITY;
 #pragma unroll
-                for (int mt = 0; mt < 2; mt++) {
+                for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                    for (int i2 = 0; i2 < 4; i2++) {
-                        const int kp = k0 + mt * 16 + 4 * lgrp + i2;
-                        float x = sacc[mt][nt][i2];
-                        if (p.softcap > 0.0f) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
-                        if (!interior) {
-                            const bool ok = kp <= qpos[nt] && kp >= qlo[nt] && kp >= klo && kp <= khi;
-                            x = ok ? x : -INFINITY;
-                        }
-                        sacc[mt][nt][i2] = x;
-                        mx = fmaxf(mx, x);
-                    }
-                }
+                    for (int i2 = 0; i2 < 4; i2++) mx = fmaxf(mx, sacc[mt][nt][i2]);
                 mx = max_rows4(mx);
                 // Lazy maximum: the row's reference moves only when a score
                 // passes it by more than 8 (log2 units), so p = 2^(s - m) stays
@@ -1035,8 +1040,12 @@ int launch_bf16_staged(gla_ctx *ctx, const PrefillParams &prm, dim3 grid, int n_
                        prm, img, n_tiles);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "stage_bf16_kernel launch: %s", hipGetErrorString(e));
-    hipLaunchKernelGGL((prefill_bf16s_kernel<D>), grid, dim3(kBf16sWaves<D> * 64), 0, ctx->stream, prm,
-                       (const uint8_t *)img, n_tiles);
+    if (prm.softcap > 0.0f)
+        hipLaunchKernelGGL((prefill_bf16s_kernel<D, true>), grid, dim3(kBf16sWaves<D> * 64), 0, ctx->stream, prm,
+                           (const uint8_t *)img, n_tiles);
+    else
+        hipLaunchKernelGGL((prefill_bf16s_kernel<D, false>), grid, dim3(kBf16sWaves<D> * 64), 0, ctx->stream, prm,
+                           (const uint8_t *)img, n_tiles);
     e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "prefill_bf16s_kernel launch: %s", hipGetErrorString(e));
     return GLA_OK;
@@ -1044,7 +1053,10 @@ int launch_bf16_staged(gla_ctx *ctx, const PrefillParams &prm, dim3 grid, int n_
 
 template <int D, bool Q8>
 int launch_bf16(gla_ctx *ctx, const PrefillParams &prm, dim3 grid) {
-    hipLaunchKernelGGL((prefill_bf16_kernel<D, Q8>), grid, dim3(kBf16Waves<D> * 64), 0, ctx->stream, prm);
+    if (prm.softcap > 0.0f)
+        hipLaunchKernelGGL((prefill_bf16_kernel<D, Q8, true>), grid, dim3(kBf16Waves<D> * 64), 0, ctx->stream, prm);
+    else
+        hipLaunchKernelGGL((prefill_bf16_kernel<D, Q8, false>), grid, dim3(kBf16Waves<D> * 64), 0, ctx->stream, prm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "prefill_bf16_kernel launch: %s", hipGetErrorString(e));
     return GLA_OK;
@@ -1052,7 +1064,10 @@ int launch_bf16(gla_ctx *ctx, const PrefillParams &prm, dim3 grid) {
 
 template <int D, int NT, int NW, bool Q8>
 int launch_f32(gla_ctx *ctx, const PrefillParams &prm, dim3 grid) {
-    hipLaunchKernelGGL((prefill_f32_kernel<D, NT, NW, Q8>), grid, dim3(NW * 64), 0, ctx->stream, prm);
+    if (prm.softcap > 0.0f)
+        hipLaunchKernelGGL((prefill_f32_kernel<D, NT, NW, Q8, true>), grid, dim3(NW * 64), 0, ctx->stream, prm);
+    else
+        hipLaunchKernelGGL((prefill_f32_kernel<D, NT, NW, Q8, false>), grid, dim3(NW * 64), 0, ctx->stream, prm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "prefill_f32_kernel launch: %s", hipGetErrorString(e));
     return GLA_OK;
