@@ -134,7 +134,7 @@ __device__ __forceinline__ float word_f(const uint4 &c, int w) {
     return __uint_as_float(w == 0 ? c.x : (w == 1 ? c.y : (w == 2 ? c.z : c.w)));
 }
 
-template <int D, int GT, int NSTEP>
+template <int D, int GT, int NSTEP, bool CAP>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodeParams p) {
     constexpr int EPL = D / 8;       // elements per lane
     constexpr int EPC = 4;           // floats per 16-byte chunk
@@ -240,7 +240,9 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
                 // q_mul on the score, not on q: q's loads then have no use
                 // before the K/V loads are issued, so their wait comes after
                 float x = sum8(dot[g]) * p.q_mul;
-                if (p.softcap > 0.0f) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
+                // (a template argument: a runtime test here became a branch
+                // around every score)
+                if constexpr (CAP) x = p.softcap * tanh_approx(x / p.softcap) * kLog2e;
                 t[s][g] = x;
             }
         }
@@ -439,7 +441,12 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(const DecodePa
 
 template <int D, int GT>
 int launch_typed(gla_ctx *ctx, const DecodeParams &prm, dim3 grid, bool combine) {
-    hipLaunchKernelGGL((decode_split_kernel<D, GT, kStepsPerIter>), grid, dim3(kThreads), 0, ctx->stream, prm);
+    if (prm.softcap > 0.0f)
+        hipLaunchKernelGGL((decode_split_kernel<D, GT, kStepsPerIter, true>), grid, dim3(kThreads), 0, ctx->stream,
+                           prm);
+    else
+        hipLaunchKernelGGL((decode_split_kernel<D, GT, kStepsPerIter, false>), grid, dim3(kThreads), 0, ctx->stream,
+                           prm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "decode_split_kernel launch: %s", hipGetErrorString(e));
     if (combine) {
