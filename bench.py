@@ -435,7 +435,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU: the attention path has no multi-GPU leg "
-                                   "(sharding is described in DESIGN.md); run with --gpus 1"}))
+                                   "(decode would shard a sequence's pages across GPUs and merge the "
+                                   "log-sum-exp partials); run with --gpus 1"}))
         return 2
 
     be = GpuBackend(0)
