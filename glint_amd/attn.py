@@ -244,7 +244,10 @@ def _hip() -> C.CDLL:
                                                   C.c_size_t]),
                          ("hipGraphLaunch", [C.c_void_p, C.c_void_p]),
                          ("hipGraphExecDestroy", [C.c_void_p]),
-                         ("hipGraphDestroy", [C.c_void_p])):
+                         ("hipGraphDestroy", [C.c_void_p]),
+                         ("hipStreamCreateWithFlags", [C.POINTER(C.c_void_p), C.c_uint]),
+                         ("hipStreamDestroy", [C.c_void_p]),
+                         ("hipStreamSynchronize", [C.c_void_p])):
             f = getattr(_HIP, fn)
             f.argtypes, f.restype = args, C.c_int
     return _HIP
@@ -255,13 +258,42 @@ def _hip_check(rc: int, what: str) -> None:
         raise GlaError(_lib.GLA_ERR_DEVICE, f"{what}: hipError {rc}")
 
 
+class HipStream:
+    """A HIP stream of default priority (non-blocking), for running library work on more than
+    one stream of a backend (GpuBackend.set_stream)."""
+
+    def __init__(self):
+        s = C.c_void_p()
+        _hip_check(_hip().hipStreamCreateWithFlags(C.byref(s), 1), "hipStreamCreateWithFlags")
+        self.ptr = s
+
+    @property
+    def handle(self) -> int:
+        return int(self.ptr.value or 0)
+
+    def synchronize(self) -> None:
+        _hip_check(_hip().hipStreamSynchronize(self.ptr), "hipStreamSynchronize")
+
+    def destroy(self) -> None:
+        if self.ptr:
+            _hip().hipStreamDestroy(self.ptr)
+            self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
 class HipGraph:
     """Library calls captured on a backend's stream and replayed with one hipGraphLaunch.
     A replay repeats the captured launches exactly: the same buffers (whose contents may
     change between replays), shapes and host-side launch decisions -- and the same context
-    scratch. A call on the backend that needs more scratch than any captured call reallocates
-    it and leaves the graph pointing at freed memory: size the scratch first (run the largest
-    calls before capturing), or capture on a GpuBackend of its own."""
+    scratch. A later call that needs more scratch moves to a larger buffer and keeps the old
+    one allocated until the context is destroyed, so the graph's pointers stay valid. A
+    captured gla_decode must be sized for the lengths of every replay: pass max_kv_len = the
+    capacity and no host lengths (the library refuses host lengths during a capture)."""
 
     def __init__(self, backend: "GpuBackend", graph: C.c_void_p, exe: C.c_void_p):
         self.backend, self.graph, self.exe = backend, graph, exe
@@ -313,6 +345,11 @@ class GpuBackend:
     def stream(self) -> int:
         return int(_lib.lib().gla_get_stream(self.ctx) or 0)
 
+    def set_stream(self, stream: Optional["HipStream"]) -> None:
+        """Enqueue later calls on `stream` (None: the backend's own stream). Work on different
+        streams uses different scratch buffers, so calls may overlap across streams."""
+        check(_lib.lib().gla_set_stream(self.ctx, stream.ptr if stream is not None else None))
+
     @property
     def cu_count(self) -> int:
         return int(_lib.lib().gla_device_cu_count(self.ctx))
@@ -329,8 +366,12 @@ class GpuBackend:
         graph = C.c_void_p()
         try:
             calls()
-        finally:
-            rc = hip.hipStreamEndCapture(stream, C.byref(graph))
+        except BaseException:
+            hip.hipStreamEndCapture(stream, C.byref(graph))
+            if graph:
+                hip.hipGraphDestroy(graph)
+            raise
+        rc = hip.hipStreamEndCapture(stream, C.byref(graph))
         _hip_check(rc, "hipStreamEndCapture")
         exe = C.c_void_p()
         rc = hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0)

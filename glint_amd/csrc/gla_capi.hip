@@ -66,8 +66,28 @@ static int grow(gla_ctx *ctx, void **ptr, size_t *cur, size_t need, bool pinned)
     return GLA_OK;
 }
 
-int ensure_scratch(gla_ctx *ctx, size_t bytes) {
-    return grow(ctx, &ctx->scratch, &ctx->scratch_bytes, bytes, false);
+int ensure_scratch(gla_ctx *ctx, size_t bytes, void **out) {
+    *out = nullptr;
+    gla_ctx::StreamScratch *ss = nullptr;
+    for (auto &e : ctx->scratch)
+        if (e.stream == ctx->stream) ss = &e;
+    if (!ss) {
+        ctx->scratch.push_back({ctx->stream, nullptr, 0});
+        ss = &ctx->scratch.back();
+    }
+    int rc = grow(ctx, &ss->ptr, &ss->bytes, bytes, false);
+    if (rc == GLA_OK) *out = ss->ptr;
+    return rc;
+}
+
+int decode_scratch(gla_ctx *ctx, const DecodeLaunch &d, size_t bytes, void **out) {
+    if (!d.scratch) return ensure_scratch(ctx, bytes, out);
+    *out = nullptr;
+    if (bytes > d.scratch_cap)
+        return set_error(GLA_ERR_INVALID, "decode needs %zu bytes of scratch; the fixed buffer holds %zu", bytes,
+                         d.scratch_cap);
+    *out = d.scratch;
+    return GLA_OK;
 }
 int ensure_dstage(gla_ctx *ctx, size_t bytes) {
     return grow(ctx, &ctx->dstage, &ctx->dstage_bytes, bytes, false);
@@ -77,6 +97,19 @@ int ensure_hstage(gla_ctx *ctx, size_t bytes) {
 }
 
 static bool head_dim_ok(int d) { return d == 64 || d == 128 || d == 256; }
+
+// Waits for the context's stream when it goes out of scope unless released:
+// a host-pointer entry point that queued a copy out of the pinned staging
+// buffer and then fails must not return while that copy is pending (the
+// next call rewrites the staging buffer).
+struct SyncOnExit {
+    hipStream_t stream;
+    bool armed = true;
+    explicit SyncOnExit(hipStream_t s) : stream(s) {}
+    ~SyncOnExit() {
+        if (armed) (void)hipStreamSynchronize(stream);
+    }
+};
 
 static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -138,7 +171,8 @@ int gla_destroy(gla_ctx *ctx) {
     if (!ctx) return GLA_OK;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    for (const auto &e : ctx->scratch)
+        if (e.ptr) (void)hipFree(e.ptr);
     if (ctx->dstage) (void)hipFree(ctx->dstage);
     if (ctx->hstage) (void)hipHostFree(ctx->hstage);
     for (const auto &r : ctx->retired) {
@@ -351,10 +385,12 @@ int gla_kv_write_rows_host(gla_ctx *ctx, gla_kv *kv, const int64_t *rows, const 
     memcpy(h, rows, (size_t)n_rows * 8);
     memcpy(h + rb, k, (size_t)n_rows * kv->kv_dim * 4);
     memcpy(h + rb + fb, v, (size_t)n_rows * kv->kv_dim * 4);
+    SyncOnExit pending(ctx->stream);
     GLA_CHECK_HIP(hipMemcpyAsync(d, h, total, hipMemcpyHostToDevice, ctx->stream), GLA_ERR_BUFFER);
     rc = launch_write_rows(ctx, kv, (const int64_t *)d, (const float *)(d + rb), (const float *)(d + rb + fb),
                            n_rows);
     if (rc != GLA_OK) return rc;
+    pending.armed = false;
     GLA_CHECK_HIP(hipStreamSynchronize(ctx->stream), GLA_ERR_KERNEL);
     return GLA_OK;
     GLA_GUARD_END
@@ -378,10 +414,12 @@ int gla_kv_export_rows_host(gla_ctx *ctx, const gla_kv *kv, const int64_t *rows,
     uint8_t *h = (uint8_t *)ctx->hstage;
     uint8_t *d = (uint8_t *)ctx->dstage;
     memcpy(h, rows, (size_t)n_rows * 8);
+    SyncOnExit pending(ctx->stream);
     GLA_CHECK_HIP(hipMemcpyAsync(d, h, (size_t)n_rows * 8, hipMemcpyHostToDevice, ctx->stream), GLA_ERR_BUFFER);
     rc = launch_export_rows(ctx, kv, (const int64_t *)d, n_rows, d + rb, d + rb + ob);
     if (rc != GLA_OK) return rc;
     GLA_CHECK_HIP(hipMemcpyAsync(h + rb, d + rb, 2 * ob, hipMemcpyDeviceToHost, ctx->stream), GLA_ERR_BUFFER);
+    pending.armed = false;
     GLA_CHECK_HIP(hipStreamSynchronize(ctx->stream), GLA_ERR_KERNEL);
     memcpy(k_out, h + rb, (size_t)n_rows * row_bytes);
     memcpy(v_out, h + rb + ob, (size_t)n_rows * row_bytes);
@@ -409,9 +447,11 @@ int gla_kv_import_rows_host(gla_ctx *ctx, gla_kv *kv, const int64_t *rows, int n
     memcpy(h, rows, (size_t)n_rows * 8);
     memcpy(h + rb, k_in, (size_t)n_rows * row_bytes);
     memcpy(h + rb + ib, v_in, (size_t)n_rows * row_bytes);
+    SyncOnExit pending(ctx->stream);
     GLA_CHECK_HIP(hipMemcpyAsync(d, h, total, hipMemcpyHostToDevice, ctx->stream), GLA_ERR_BUFFER);
     rc = launch_import_rows(ctx, kv, (const int64_t *)d, n_rows, d + rb, d + rb + ib);
     if (rc != GLA_OK) return rc;
+    pending.armed = false;
     GLA_CHECK_HIP(hipStreamSynchronize(ctx->stream), GLA_ERR_KERNEL);
     return GLA_OK;
     GLA_GUARD_END
@@ -504,6 +544,15 @@ int gla_decode(gla_ctx *ctx, const gla_decode_args *a) {
     d.kv_start_host = a->kv_start_host;
     d.kv_len_host = a->kv_len_host;
     GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
+    if (a->kv_len_host) {
+        // The host lengths size the launch; a captured graph would replay
+        // that sizing after the device lengths have grown.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        GLA_CHECK_HIP(hipStreamIsCapturing(ctx->stream, &cs), GLA_ERR_DEVICE);
+        GLA_REQUIRE(cs == hipStreamCaptureStatusNone,
+                    "gla_decode: host lengths are not allowed while the stream is being captured (a graph replay "
+                    "would keep the launch sized for them); pass max_kv_len = the capacity and no host lengths");
+    }
     return launch_decode(ctx, d);
     GLA_GUARD_END
 }
@@ -572,6 +621,7 @@ int gla_attention(gla_ctx *ctx, const float *q, const float *k, const float *v, 
     int32_t *ints = (int32_t *)(h + 2 * qb + 2 * kb);
     ints[0] = 0;
     ints[1] = seq_len;
+    SyncOnExit pending(ctx->stream);
     GLA_CHECK_HIP(hipMemcpyAsync(d, h, qb, hipMemcpyHostToDevice, ctx->stream), GLA_ERR_BUFFER);
     GLA_CHECK_HIP(hipMemcpyAsync(d + 2 * qb, h + 2 * qb, 2 * kb + ib, hipMemcpyHostToDevice, ctx->stream),
                   GLA_ERR_BUFFER);
@@ -607,6 +657,7 @@ int gla_attention(gla_ctx *ctx, const float *q, const float *k, const float *v, 
     GLA_CHECK_HIP(hipMemcpyAsync(h + qb, d + qb, (size_t)n_heads * head_dim * 4, hipMemcpyDeviceToHost,
                                  ctx->stream),
                   GLA_ERR_BUFFER);
+    pending.armed = false;
     GLA_CHECK_HIP(hipStreamSynchronize(ctx->stream), GLA_ERR_KERNEL);
     memcpy(out, h + qb, (size_t)n_heads * head_dim * 4);
     return GLA_OK;
@@ -637,6 +688,7 @@ int gla_attention_resident(gla_ctx *ctx, const float *q, const gla_kv *cache, in
     ints[0] = window_start;
     ints[1] = attend_len;
     ints[2] = seq;
+    SyncOnExit pending(ctx->stream);
     GLA_CHECK_HIP(hipMemcpyAsync(d, h, qb, hipMemcpyHostToDevice, ctx->stream), GLA_ERR_BUFFER);
     GLA_CHECK_HIP(hipMemcpyAsync(d + 2 * qb, h + 2 * qb, 256, hipMemcpyHostToDevice, ctx->stream),
                   GLA_ERR_BUFFER);
@@ -661,6 +713,7 @@ int gla_attention_resident(gla_ctx *ctx, const float *q, const gla_kv *cache, in
     GLA_CHECK_HIP(hipMemcpyAsync(h + qb, d + qb, (size_t)n_heads * cache->head_dim * 4, hipMemcpyDeviceToHost,
                                  ctx->stream),
                   GLA_ERR_BUFFER);
+    pending.armed = false;
     GLA_CHECK_HIP(hipStreamSynchronize(ctx->stream), GLA_ERR_KERNEL);
     memcpy(out, h + qb, (size_t)n_heads * cache->head_dim * 4);
     return GLA_OK;

@@ -4,7 +4,7 @@
 // batch, as attn_heads_cpu runs it (src/transformer/forward.rs:240-270).
 //
 // Work decomposition (split-K / flash-decoding):
-//   grid = (split, kv_head x head_group, sequence), 256 threads (4 waves).
+//   grid = (kv_head x head_group, split, sequence), 256 threads (4 waves).
 //   A workgroup owns `pps` consecutive pages of one sequence and one KV head,
 //   and all GT q-heads that read that KV head (GQA: K/V are read once for the
 //   whole group). Each wave takes whole pages; inside a wave 8 lanes share a
@@ -13,6 +13,10 @@
 //   tokens. A lane group keeps its own online-softmax state (m, l, acc) in
 //   the log2 domain; the groups are merged with shuffles once per split, the
 //   4 waves through LDS, and splits by decode_combine_kernel.
+// Batch invariance: `pps` is a function of the sequence's own window
+// (split_pages), so where its splits fall, and with them every rounding of
+// its result, is the same whatever else is in the batch -- the reference's
+// batched == single guarantee (src/transformer/forward.rs:1946-2002).
 // This file serves f32 storage; Q8_0 storage has its own MFMA kernel
 // (gla_decode_q8.hip).
 #include <float.h>
@@ -45,7 +49,7 @@ struct DecodeParams {
     int n_kv_heads;
     int group;  // n_heads / n_kv_heads
     int n_hg;   // head groups per kv head
-    int pps;    // pages per split
+    int pps_fixed;  // pages per split for every window (tuning override), or 0: split_pages
     int max_splits;
     int max_len;  // host bound on kv_len: lengths are clamped to it, so splits never exceed max_splits
     float q_mul;    // multiplier of q.k: scale*log2(e), or scale with a soft-cap
@@ -92,11 +96,29 @@ __device__ __forceinline__ float tanh_approx(float x) {
     return copysignf(r, x);
 }
 
+// Pages per split of a window spanning n pages: 4 up to 128 pages, 8 up to
+// 256, 12 up to 384, then 16. A function of the window alone (see the file
+// comment); it gives a single sequence enough splits to spread over the
+// chip (cfg2, 256 pages: 32 splits of 8 measured 14.6 us per layer against
+// 16.1 with 64 of 4 and 16.4 with 16 of 16; cfg1, 32 pages: 8 splits of 4
+// pages, 7.6 us per call, against 8.3 with 8-page splits).
+__host__ __device__ __forceinline__ int split_pages(int n_pages) {
+    const int p = 4 * ((n_pages + 127) / 128);
+    return p < 4 ? 4 : (p > 16 ? 16 : p);
+}
+
+// The most splits split_pages gives any window of at most n pages.
+int max_splits_upto(int n) {
+    if (n <= 128) return (n + 3) / 4;
+    return std::max(32, (n + 15) / 16);
+}
+
 // Range of pages and splits of sequence b, after clamping to the storage.
 struct SeqRange {
     int start, end;  // positions [start, end)
     int fp;          // first logical page
     int n_pages;
+    int pps;         // pages per split
     int n_splits;
 };
 
@@ -114,10 +136,12 @@ __device__ __forceinline__ SeqRange seq_range(const DecodeParams &p, int b) {
     if (e > s) {
         r.fp = s >> 4;
         r.n_pages = ((e - 1) >> 4) - r.fp + 1;
-        r.n_splits = (r.n_pages + p.pps - 1) / p.pps;
+        r.pps = p.pps_fixed > 0 ? p.pps_fixed : split_pages(r.n_pages);
+        r.n_splits = min((r.n_pages + r.pps - 1) / r.pps, p.max_splits);
     } else {
         r.fp = 0;
         r.n_pages = 0;
+        r.pps = 1;
         r.n_splits = 0;
     }
     return r;
@@ -164,8 +188,10 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
         return;
     }
     if (split >= r.n_splits) return;
-    const int pg0 = r.fp + split * p.pps;
-    const int pg1 = min(r.fp + r.n_pages, pg0 + p.pps);
+    const int pg0 = r.fp + split * r.pps;
+    // (the last split takes what is left; it only differs from pg0 + pps when
+    // the device lengths exceed what max_splits was sized for)
+    const int pg1 = split + 1 == r.n_splits ? r.fp + r.n_pages : min(r.fp + r.n_pages, pg0 + r.pps);
 
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -497,27 +523,18 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
     const int group = d.n_heads / d.n_kv_heads;
     const int gt = pick_gt(D, group);
     const int n_hg = (group + gt - 1) / gt;
-    const int ppw = kStepsPerIter / 2;  // pages per wave per iteration
 
     // pages a window can span (a start inside a page adds one)
     const int max_pages = d.max_kv_len > 0 ? (d.max_kv_len + GLA_PAGE_SIZE - 1) / GLA_PAGE_SIZE + 1 : 1;
     const int64_t units = (int64_t)d.n_seqs * d.n_kv_heads * n_hg;
-    // About one workgroup per CU over the longest window (of max_kv_len
-    // positions; a start inside a page is left out of the sizing), at most
-    // 16 pages a split: at cfg2 (one sequence, 4,096 positions, 8 KV heads)
-    // 8-page splits measured 14.6 us per layer against 16.1 at 4 pages (twice
-    // the workgroups and partials), 16.4 at 16 and 22.7 at 32.
-    const int64_t target = std::max(ctx->n_cu, 1);
-    const int64_t splits_t = std::max<int64_t>(1, (target + units - 1) / units);
-    const int span = std::max(1, (d.max_kv_len + GLA_PAGE_SIZE - 1) / GLA_PAGE_SIZE);
-    int pps = (int)std::max<int64_t>(1, (span + splits_t - 1) / splits_t);
-    const int quantum = kWaves * ppw;
-    pps = std::min((pps + quantum - 1) / quantum * quantum, std::max(16, quantum));
+    // Split sizes come from each window alone (split_pages); GLA_DECODE_PPS
+    // forces one size for every window (tuning only).
+    int pps_fixed = 0;
     if (const char *env = getenv("GLA_DECODE_PPS")) {
-        int v = atoi(env);
-        if (v > 0) pps = v;
+        const int v = atoi(env);
+        if (v > 0) pps_fixed = v;
     }
-    const int max_splits = (max_pages + pps - 1) / pps;
+    const int max_splits = pps_fixed > 0 ? (max_pages + pps_fixed - 1) / pps_fixed : max_splits_upto(max_pages);
 
     DecodeParams prm;
     prm.kv = d.kv;
@@ -530,7 +547,7 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
     prm.n_kv_heads = d.n_kv_heads;
     prm.group = group;
     prm.n_hg = n_hg;
-    prm.pps = pps;
+    prm.pps_fixed = pps_fixed;
     prm.max_splits = max_splits;
     prm.max_len = d.max_kv_len;
     const bool cap = d.softcap > 0.0f;
@@ -542,10 +559,11 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
         const size_t slots = (size_t)units * max_splits;
         const size_t acc_b = slots * gt * D * sizeof(float);
         const size_t ml_b = slots * gt * 2 * sizeof(float);
-        int rc = ensure_scratch(ctx, acc_b + ml_b);
+        void *scr = nullptr;
+        int rc = decode_scratch(ctx, d, acc_b + ml_b, &scr);
         if (rc != GLA_OK) return rc;
-        prm.part_acc = (float *)ctx->scratch;
-        prm.part_ml = (float *)((uint8_t *)ctx->scratch + acc_b);
+        prm.part_acc = (float *)scr;
+        prm.part_ml = (float *)((uint8_t *)scr + acc_b);
     }
     if (d.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "decode: n_seqs %d > 65535", d.n_seqs);
     if (max_splits > 65535) return set_error(GLA_ERR_INVALID, "decode: %d splits per sequence > 65535", max_splits);

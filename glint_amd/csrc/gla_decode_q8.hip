@@ -39,12 +39,19 @@
 // packed subtract per two elements.
 // The 4 waves of a workgroup merge their chunks (log-sum-exp) in LDS; units
 // longer than a workgroup are merged by a second, small kernel.
+//
+// Batch invariance (the reference's batched == single guarantee,
+// src/transformer/forward.rs:1946-2002): a sequence's chunks, workgroups and
+// merge order depend on its own window and head_dim only, never on the rest
+// of the batch. What adapts to the batch is how many q-heads a wave carries
+// (hpw): a head owns its own MFMA columns (S) and rows (P'.V), its own
+// maximum, sum and q scale, so its result does not depend on the heads that
+// share its wave.
 #include <math.h>
 #include <stdlib.h>
 
 #include <algorithm>
 #include <cmath>
-#include <vector>
 
 #include "gla_internal.h"
 
@@ -58,7 +65,7 @@ typedef float float2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
-constexpr int kGT = 4;  // q-heads per wave
+constexpr int kGT = 4;  // q-heads a wave can carry (MFMA column / row groups)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxChunks = 64;  // preferred bound on chunks per unit
 // Workgroup rows listed in the launch arguments (see Q8Params::rows): 3 KB of
@@ -78,7 +85,8 @@ struct Q8Params {
     int n_heads;
     int n_kv_heads;
     int group;
-    int n_hg;
+    int hpw;     // q-heads per wave (1..kGT)
+    int n_hg;    // head groups per KV head: ceil(group / hpw)
     int ch;      // pages per chunk (even)
     int max_wg;  // workgroups per unit (partials per unit)
     int max_len;
@@ -728,8 +736,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
     }
     const int kvh = blockIdx.x / p.n_hg;
     const int hg = blockIdx.x - kvh * p.n_hg;
-    const int g0 = hg * kGT;
-    const int gcount = min(kGT, p.group - g0);
+    const int g0 = hg * p.hpw;
+    const int gcount = min(p.hpw, p.group - g0);
     const int h_base = kvh * p.group + g0;
     float *out = p.out + ((int64_t)b * p.n_heads + h_base) * D;
 
@@ -808,8 +816,8 @@ __global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p
     const int b = blockIdx.z;
     const int kvh = blockIdx.y / p.n_hg;
     const int hg = blockIdx.y - kvh * p.n_hg;
-    const int g0 = hg * kGT;
-    const int gcount = min(kGT, p.group - g0);
+    const int g0 = hg * p.hpw;
+    const int gcount = min(p.hpw, p.group - g0);
     const int h_base = kvh * p.group + g0;
     const Range r = seq_range(p, b);
     const int span = kWaves * p.ch;  // pages per workgroup
@@ -890,29 +898,36 @@ int host_seq_pages(int start, int len, int max_len, int pos_limit) {
     return e > s ? (int)(((e - 1) >> 4) - (s >> 4) + 1) : 0;
 }
 
-// Pages per chunk: 28 (14 steps) for head_dim up to 128, 40 for 256,
-// measured best on the Llama-3-8B and Gemma-2-9B batch decodes with the
-// workgroups dispatched longest first (shorter chunks repeat the q / page-id
-// / V-scale set-up more often, longer ones leave the grid's last workgroups
-// running alone; 20 was best before the longest-first order, which takes
-// most of that tail away). A batch too small to give every resident
-// workgroup slot a workgroup at that size gets shorter chunks, down to 2.
-// With the pages of every sequence known (np) the counts are exact; without
-// them every sequence is taken to span max_pages.
-int choose_chunk_pages(const std::vector<int> &np, int n_seqs, int max_pages, int n_hu, int64_t slots, int D) {
-    // at most 64 pages per wave (one page id per lane), even past kMaxChunks chunks
-    const int lo = std::min(64, std::max(2, (max_pages + kMaxChunks - 1) / kMaxChunks));
-    int ch = std::min(64, std::max(D == 256 ? 40 : 28, (lo + 1) & ~1));
-    for (; ch > 2 && ch - 2 >= lo; ch -= 2) {
-        int64_t wgs = 0;
-        if (np.empty()) {
-            wgs = (int64_t)n_seqs * (((max_pages + ch - 1) / ch + kWaves - 1) / kWaves);
-        } else {
-            for (int n : np) wgs += ((n + ch - 1) / ch + kWaves - 1) / kWaves;
-        }
-        if (wgs * n_hu >= slots) break;
+// Pages per chunk: 28 (14 steps) for head_dim up to 128, 40 for 256, for
+// every window (a chunk holds at most 64 pages, one page id per lane).
+// Measured on the Llama-3-8B and Gemma-2-9B batch decodes with the workgroups
+// dispatched longest first: shorter chunks repeat the q / page-id / V-scale
+// set-up more often, longer ones leave the grid's last workgroups running
+// alone. Fixed rather than fitted to the batch, so that a sequence's result
+// is the same in any batch.
+int chunk_pages(int D) { return D == 256 ? 40 : 28; }
+
+// q-heads per wave: kGT (or the group, if smaller), lowered only while the
+// workgroups that result still fit the device's resident slots in one round.
+// Fewer heads per wave multiply the workgroups of a small batch (each (page,
+// KV head) span is then read by group / hpw waves, dispatched together, the
+// later reads served by L2), at the price of repeating the per-wave work; a
+// batch that already fills most of the slots loses by it (Gemma-2's 4096
+// window at B=32, 410 workgroups on 512 slots: 165 against ~110 us).
+int choose_hpw(int group, int64_t wg_per_hg, int n_kv_heads, int64_t slots) {
+    int hpw = std::min(kGT, group);
+    int n_hg = (group + hpw - 1) / hpw;
+    while (hpw > 1) {
+        // the next head-group count that lowers the heads per wave (balanced
+        // groups: 4 heads go 4 -> 2 + 2 -> 1 + 1 + 1 + 1)
+        int h = hpw, m = n_hg;
+        while (h == hpw) h = (group + (++m) - 1) / m;
+        m = (group + h - 1) / h;
+        if (wg_per_hg * n_kv_heads * m > slots) break;
+        hpw = h;
+        n_hg = m;
     }
-    return ch;
+    return hpw;
 }
 
 }  // namespace
@@ -920,30 +935,37 @@ int choose_chunk_pages(const std::vector<int> &np, int n_seqs, int max_pages, in
 int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
     const int D = d.head_dim;
     const int group = d.n_heads / d.n_kv_heads;
-    const int n_hg = (group + kGT - 1) / kGT;
     // pages a window can span (a start inside a page adds one)
     const int64_t max_pages = d.max_kv_len > 0 ? (d.max_kv_len + GLA_PAGE_SIZE - 1) / GLA_PAGE_SIZE + 1 : 1;
-    const int64_t units = (int64_t)d.n_seqs * d.n_kv_heads * n_hg;
-    // Chunk size (pages per wave; even, and at most 64: a wave holds one page
-    // id per lane). See choose_chunk_pages.
-    std::vector<int> np;
-    if (d.kv_len_host) {
-        np.resize(d.n_seqs);
-        for (int b = 0; b < d.n_seqs; b++)
-            np[b] = host_seq_pages(d.kv_start_host[b], d.kv_len_host[b], d.max_kv_len, d.pm.pos_limit);
-    }
-    int per_cu = D == 64 ? resident_wgs<64>() : (D == 128 ? resident_wgs<128>() : resident_wgs<256>());
-    const int64_t slots = (int64_t)std::max(ctx->n_cu, 1) * std::max(per_cu, 1);
-    int64_t ch = choose_chunk_pages(np, d.n_seqs, (int)max_pages, d.n_kv_heads * n_hg, slots, D);
+    const bool host = d.kv_len_host != nullptr;
+    auto pages_of = [&](int b) -> int {
+        return host ? host_seq_pages(d.kv_start_host[b], d.kv_len_host[b], d.max_kv_len, d.pm.pos_limit)
+                    : (int)max_pages;
+    };
+    // Chunk size (pages per wave; even, at most 64). GLA_Q8_CHUNK_PAGES
+    // forces another size (tuning and tests).
+    int ch = chunk_pages(D);
     if (const char *env = getenv("GLA_Q8_CHUNK_PAGES")) {
         const int v = atoi(env);
         if (v > 0) ch = std::min(64, (v + 1) & ~1);
     }
+    const int span = kWaves * ch;  // pages per workgroup
     // workgroups per unit: exact with host lengths, else the max_kv_len bound
-    int64_t max_pages_seen = max_pages;
-    if (!np.empty()) max_pages_seen = std::max(1, *std::max_element(np.begin(), np.end()));
-    const int64_t max_chunks = (max_pages_seen + ch - 1) / ch;
-    const int64_t max_wg = (max_chunks + kWaves - 1) / kWaves;
+    int64_t max_wg = 1, wg_total = 0;
+    for (int b = 0; b < d.n_seqs; b++) {
+        const int64_t nw = ((int64_t)pages_of(b) + span - 1) / span;
+        max_wg = std::max(max_wg, nw);
+        wg_total += std::max<int64_t>(nw, 1);
+    }
+    const int per_cu = D == 64 ? resident_wgs<64>() : (D == 128 ? resident_wgs<128>() : resident_wgs<256>());
+    const int64_t slots = (int64_t)std::max(ctx->n_cu, 1) * std::max(per_cu, 1);
+    int hpw = choose_hpw(group, wg_total, d.n_kv_heads, slots);
+    if (const char *env = getenv("GLA_Q8_HEADS_PER_WAVE")) {
+        const int v = atoi(env);
+        if (v > 0) hpw = std::min(std::min(v, kGT), group);
+    }
+    const int n_hg = (group + hpw - 1) / hpw;
+    const int64_t units = (int64_t)d.n_seqs * d.n_kv_heads * n_hg;
 
     Q8Params prm;
     prm.base = d.kv.k;
@@ -957,42 +979,51 @@ int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
     prm.n_heads = d.n_heads;
     prm.n_kv_heads = d.n_kv_heads;
     prm.group = group;
+    prm.hpw = hpw;
     prm.n_hg = n_hg;
-    prm.ch = (int)ch;
-    prm.max_wg = (int)max_wg;
+    prm.ch = ch;
+    prm.max_wg = (int)std::min<int64_t>(max_wg, 1 << 30);
     prm.max_len = d.max_kv_len;
     const bool cap = d.softcap > 0.0f;
     prm.q_mul = cap ? d.scale : d.scale * kLog2e;
     prm.softcap = cap ? d.softcap : 0.0f;
     prm.part = nullptr;
+    if (d.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "decode: n_seqs %d > 65535", d.n_seqs);
+    if (max_wg > 65535)
+        return set_error(GLA_ERR_INVALID, "decode: %lld workgroups per sequence > 65535", (long long)max_wg);
     if (max_wg > 1) {
         const size_t bytes = (size_t)units * max_wg * kGT * (D + 2) * sizeof(float);
-        int rc = ensure_scratch(ctx, bytes);
+        void *scr = nullptr;
+        int rc = decode_scratch(ctx, d, bytes, &scr);
         if (rc != GLA_OK) return rc;
-        prm.part = (float *)ctx->scratch;
+        prm.part = (float *)scr;
     }
-    if (d.n_seqs > 65535) return set_error(GLA_ERR_INVALID, "decode: n_seqs %d > 65535", d.n_seqs);
-    if (max_wg > 65535) return set_error(GLA_ERR_INVALID, "decode: %lld workgroups per sequence > 65535", (long long)max_wg);
     dim3 grid(d.n_kv_heads * n_hg, (unsigned)max_wg, d.n_seqs);
     // With the host lengths, list the workgroups that have pages (plus one per
     // empty window, which zeroes its output), longest first: the dispatcher
     // then starts the full workgroups before the short last ones of each
-    // sequence, which fill in at the end.
+    // sequence, which fill in at the end. A counting sort over the page
+    // counts (0 .. span) keeps the order stable and allocates nothing.
     prm.n_rows = 0;
-    if (!np.empty() && max_wg <= 64 && d.n_seqs <= 1024) {
-        const int span = kWaves * (int)ch;
-        std::vector<std::pair<int, uint16_t>> w;
-        w.reserve(kMaxRows + 1);
-        for (int b = 0; b < d.n_seqs && w.size() <= (size_t)kMaxRows; b++) {
-            if (np[b] == 0) w.push_back({0, (uint16_t)(b << 6)});
-            for (int j = 0; j * span < np[b]; j++) w.push_back({std::min(span, np[b] - j * span), (uint16_t)(b << 6 | j)});
+    if (host && max_wg <= 64 && d.n_seqs <= 1024 && wg_total <= kMaxRows) {
+        int count[4 * 64 + 2] = {0};  // rows per page count, span <= 256
+        auto wg_pages = [&](int n, int j) { return n == 0 ? 0 : std::min(span, n - j * span); };
+        for (int b = 0; b < d.n_seqs; b++) {
+            const int n = pages_of(b);
+            for (int j = 0; j == 0 || j * span < n; j++) count[wg_pages(n, j)]++;
         }
-        if (w.size() <= (size_t)kMaxRows) {
-            std::stable_sort(w.begin(), w.end(), [](const auto &x, const auto &y) { return x.first > y.first; });
-            for (size_t i = 0; i < w.size(); i++) prm.rows[i] = w[i].second;
-            prm.n_rows = (int)w.size();
-            grid = dim3(d.n_kv_heads * n_hg, (unsigned)w.size(), 1);
+        int at[4 * 64 + 2];  // first row of each page count, longest first
+        int next = 0;
+        for (int c = span; c >= 0; c--) {
+            at[c] = next;
+            next += count[c];
         }
+        for (int b = 0; b < d.n_seqs; b++) {
+            const int n = pages_of(b);
+            for (int j = 0; j == 0 || j * span < n; j++) prm.rows[at[wg_pages(n, j)]++] = (uint16_t)(b << 6 | j);
+        }
+        prm.n_rows = next;
+        grid = dim3(d.n_kv_heads * n_hg, (unsigned)next, 1);
     }
     switch (D) {
     case 64:

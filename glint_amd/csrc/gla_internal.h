@@ -119,9 +119,15 @@ struct gla_ctx {
     int n_cu = 0;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
-    // split-K partials of decode
-    void *scratch = nullptr;
-    size_t scratch_bytes = 0;
+    // Device scratch (decode partials, bf16 tile images, matvec pieces), one
+    // buffer per stream the context has launched work on: work queued on two
+    // streams at once never shares a buffer.
+    struct StreamScratch {
+        hipStream_t stream;
+        void *ptr;
+        size_t bytes;
+    };
+    std::vector<StreamScratch> scratch;
     // device and pinned host staging of the host-pointer entry points
     void *dstage = nullptr;
     size_t dstage_bytes = 0;
@@ -154,7 +160,9 @@ struct gla_kv {
 namespace gla {
 
 KvLayout layout_of(const gla_kv *kv);
-int ensure_scratch(gla_ctx *ctx, size_t bytes);
+// At least `bytes` of device scratch for work on ctx->stream (grown by
+// doubling; a replaced buffer stays allocated until gla_destroy).
+int ensure_scratch(gla_ctx *ctx, size_t bytes, void **out);
 int ensure_dstage(gla_ctx *ctx, size_t bytes);
 int ensure_hstage(gla_ctx *ctx, size_t bytes);
 
@@ -176,7 +184,15 @@ struct DecodeLaunch {
     float *out;
     const int32_t *kv_start_host = nullptr;  // optional host copies (both or neither)
     const int32_t *kv_len_host = nullptr;
+    // A caller-provided scratch buffer of scratch_cap bytes: when set the
+    // launch allocates nothing and fails with GLA_ERR_INVALID if the
+    // partials need more; when NULL the context's scratch is used.
+    void *scratch = nullptr;
+    size_t scratch_cap = 0;
 };
+// Device scratch of a decode launch: d.scratch (no allocation) or the
+// context's buffer for its current stream.
+int decode_scratch(gla_ctx *ctx, const DecodeLaunch &d, size_t bytes, void **out);
 int launch_decode(gla_ctx *ctx, const DecodeLaunch &d);
 int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d);
 

@@ -692,11 +692,12 @@ int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, f
     const size_t xs_bytes = ((size_t)vec_pad * sizeof(float) + 255) / 256 * 256;
     const int64_t split_stride = (int64_t)16 * kMaxVT * w->rows;  // one slice of partials: 64 vectors x rows
     const size_t part_bytes = n_splits > 1 ? (size_t)n_splits * split_stride * sizeof(float) : 0;
-    int rc = ensure_scratch(ctx, xp_bytes + xs_bytes + part_bytes);
+    void *scr = nullptr;
+    int rc = ensure_scratch(ctx, xp_bytes + xs_bytes + part_bytes, &scr);
     if (rc != GLA_OK) return rc;
-    _Float16 *xp = (_Float16 *)ctx->scratch;
-    float *xs = (float *)((uint8_t *)ctx->scratch + xp_bytes);
-    float *part = (float *)((uint8_t *)ctx->scratch + xp_bytes + xs_bytes);
+    _Float16 *xp = (_Float16 *)scr;
+    float *xs = (float *)((uint8_t *)scr + xp_bytes);
+    float *part = (float *)((uint8_t *)scr + xp_bytes + xs_bytes);
     const dim3 sgrid((n_blocks_pad * 4 + 256 * kSplitU - 1) / (256 * kSplitU), vec_pad);
     if (((uintptr_t)x & 15) == 0)  // rows start 128-byte apart: the base decides
         hipLaunchKernelGGL(split_x_kernel<true>, sgrid, dim3(256), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad,

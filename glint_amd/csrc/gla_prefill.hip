@@ -1154,9 +1154,10 @@ int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
     dim3 grid(a.n_seqs * a.n_kv_heads * (group / hpw), prm.n_qblocks, 1);
     if (a.precision == GLA_PREC_BF16) {
         if (staged) {
-            int rc = ensure_scratch(ctx, img_bytes);
+            void *scr = nullptr;
+            int rc = ensure_scratch(ctx, img_bytes, &scr);
             if (rc != GLA_OK) return rc;
-            uint8_t *img = (uint8_t *)ctx->scratch;
+            uint8_t *img = (uint8_t *)scr;
             switch (D) {
             case 64:
                 return a.q8 ? launch_bf16_staged<64, true>(ctx, prm, grid, a.n_seqs, img, n_tiles)

@@ -51,3 +51,25 @@ def max_errors(got, want):
     err = np.abs(got - want)
     rel = err / np.maximum(np.abs(want), 1e-30)
     return float(err.max(initial=0.0)), float(rel.max(initial=0.0))
+
+
+LOG2E_F32 = np.float32(1.4426950408889634)
+
+
+def bf16_round(x):
+    """f32 values rounded to bf16 (nearest, ties to even), returned as f32."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return r.view(np.float32)
+
+
+def bf16_prefill_inputs(q, k, v, scale, softcap=None):
+    """The values a bf16-input prefill multiplies, as f32 inputs for the fp32 oracle: K and V
+    rounded to bf16, and q as the kernel rounds it, bf16(q * mul) / mul with mul = scale (with a
+    soft-cap) or scale * log2(e) (the kernel folds the exp2 base into q). The oracle over these
+    inputs differs from the kernel only by the bf16 rounding of the probabilities and the order
+    of the fp32 sums; the gap to the oracle over the raw inputs is the input rounding, which
+    grows with the score magnitudes."""
+    mul = np.float32(scale) if softcap else np.float32(scale) * LOG2E_F32
+    qm = np.ascontiguousarray(q, np.float32) * mul
+    return bf16_round(qm) / mul, bf16_round(k), bf16_round(v)

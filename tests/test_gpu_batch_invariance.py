@@ -1,0 +1,73 @@
+"""A sequence decodes to the same bits alone as in any batch -- the reference's batched ==
+single guarantee (`assert_same_logits` compares to_bits(), src/transformer/forward.rs:1946-1954;
+checked at :1960-2002 and, for Q8_0, :2257-2308), on which its engine tests build (a paged
+pool gives the same tokens, src/server/engine.rs:1095; a forked admission is bit-identical to a
+cold one, :1836).
+
+Every sequence of a cfg3-shaped batch (Llama-3-8B heads, B=64, ctx U[128, 8192], paged, 256-token
+shared prefix) is decoded in the whole batch (with and without the host copies of the lengths,
+which size the launch), in a shuffled sub-batch, and alone, for Q8_0 and f32 pools, global and
+with a 4096-token window and soft-cap 50 (K x 3, so the cap bites). All outputs must be equal
+bit for bit. Alone, the Q8_0 path spreads the q-heads of a KV head over more waves (the batch is
+too small to fill the device otherwise), so this also checks that a head's result does not
+depend on the heads that share its wave. For f32 the host-buffer entry point
+(GpuBackend::attention, Glint's [pos][kv_head][d] layout) must give the same bits as well.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from glint_amd import synth
+from gpu_util import run_decode, write_rows_chunked
+
+pytestmark = pytest.mark.gpu
+
+H, HKV, D, B = 32, 8, 128, 64
+SCALE = float(1 / np.sqrt(D))
+
+
+def _bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def cfg3_batch():
+    ctx = synth.uniform_int(3103, 128, 8192, B)
+    pb = synth.paged_batch(3104, ctx, prefix_tokens=256)
+    rows, k, v = synth.pool_rows(3105, 3106, 0, pb.n_pages, HKV * D, 3.0)
+    q = synth.normal(3107, (B, H, D))
+    return pb, rows, k, v, q
+
+
+@pytest.mark.parametrize("dtype", ["q8", "f32"])
+def test_decode_is_batch_invariant_cfg3(backend, cfg3_batch, dtype):
+    pb, rows, k, v, q = cfg3_batch
+    pool = backend.create_page_pool(pb.n_pages, HKV, D, dtype)
+    write_rows_chunked(pool, rows, k, v)
+    sub = np.random.default_rng(3108).permutation(B)[:24]
+    try:
+        for window, cap in ((None, None), (4096, 50.0)):
+            w = synth.windowed(pb, window)
+            what = f"{dtype} window {window} cap {cap}"
+            full = run_decode(backend, pool, q, w.kv_start, w.kv_len, H, SCALE, cap, table=pb.table)
+            assert np.isfinite(full).all(), what
+            nohost = run_decode(backend, pool, q, w.kv_start, w.kv_len, H, SCALE, cap, table=pb.table,
+                                host_lengths=False)
+            assert np.array_equal(_bits(nohost), _bits(full)), f"{what}: launch sized without host lengths"
+            part = run_decode(backend, pool, q[sub], w.kv_start[sub], w.kv_len[sub], H, SCALE, cap,
+                              table=pb.table[sub])
+            for i, b in enumerate(sub):
+                assert np.array_equal(_bits(part[i]), _bits(full[b])), f"{what}: seq {b} in a shuffled sub-batch"
+            for b in range(B):
+                alone = run_decode(backend, pool, q[b:b + 1], w.kv_start[b:b + 1], w.kv_len[b:b + 1], H, SCALE,
+                                   cap, table=pb.table[b:b + 1])
+                assert np.array_equal(_bits(alone[0]), _bits(full[b])), f"{what}: seq {b} alone"
+            if dtype == "f32" and window is None:
+                for b in (int(np.argmax(pb.ctx)), int(np.argmin(pb.ctx))):
+                    pos = np.arange(int(pb.ctx[b]))
+                    r = pb.table[b, pos // 16].astype(np.int64) * 16 + pos % 16
+                    got = backend.attention(q[b].reshape(-1), k[r], v[r], H, HKV, D, len(pos), SCALE, cap)
+                    assert np.array_equal(_bits(got), _bits(full[b].reshape(-1))), f"attention() seq {b}"
+    finally:
+        pool.destroy()

@@ -1,10 +1,13 @@
 """HIP graph capture of library calls (GpuBackend.capture): a decode step's calls -- a paged
 Q8_0 batch decode, three layers of a contiguous f32 decode, a Q8_0 projection and RoPE on its
-output -- captured once and replayed. Between replays new inputs are uploaded and the same calls
-run eagerly into other buffers; every replay equals the eager calls bit for bit (the kernels are
-deterministic, and the graph must read the buffers' current contents). Before the last replays an
-eager call with a much larger scratch need (a 64-token projection of 4096 columns) makes the
-context allocate a larger scratch; the graph keeps the old buffer, which stays allocated."""
+output -- captured once and replayed. Between replays new inputs are uploaded, the sequences'
+device lengths grow (as they do from one decode step to the next), and the same calls run
+eagerly into other buffers; every replay equals the eager calls bit for bit (the kernels are
+deterministic, and the graph must read the buffers' current contents). The captured decode is
+sized for the page table's capacity and passes no host lengths (the eager one passes them, as
+the engine does); a capture with host lengths is refused. Before the last replays an eager call
+with a much larger scratch need (a 64-token projection of 4096 columns) makes the context
+allocate a larger scratch; the graph keeps the old buffer, which stays allocated."""
 from __future__ import annotations
 
 import numpy as np
@@ -12,6 +15,7 @@ import pytest
 
 import oracle as orc
 from glint_amd import synth
+from glint_amd._lib import GlaError
 from gpu_util import Contig, Pool
 
 pytestmark = pytest.mark.gpu
@@ -37,10 +41,17 @@ def test_graph_replays_equal_eager_calls(backend):
     of = [[be.empty(9 * 64 * 4) for _ in range(3)] for _ in range(2)]
     oy = [be.empty(2 * 48 * 4) for _ in range(2)]
 
+    capacity = pb.table.shape[1] * 16
+    lens = {"now": pb.kv_len.copy()}
+
     def calls(k):
-        be.decode(p.pool, dq8, o8[k], ds, dl, 4, int(pb.kv_len.max()), H, 0.088, 30.0,
-                  page_table=dt, page_table_stride=pb.table.shape[1], kv_start_host=pb.kv_start,
-                  kv_len_host=pb.kv_len)
+        if k == 0:  # eager: sized from the host lengths
+            be.decode(p.pool, dq8, o8[k], ds, dl, 4, int(lens["now"].max()), H, 0.088, 30.0,
+                      page_table=dt, page_table_stride=pb.table.shape[1], kv_start_host=pb.kv_start,
+                      kv_len_host=lens["now"])
+        else:  # captured: sized for every length a replay may see
+            be.decode(p.pool, dq8, o8[k], ds, dl, 4, capacity, H, 0.088, 30.0,
+                      page_table=dt, page_table_stride=pb.table.shape[1])
         for layer in range(3):
             be.decode(c.cache, dqf, of[k][layer], dsf, dlf, 1, 512, 9, 0.125, layer=layer)
         be.matvec_q8_0(w, dx, 2, oy[k])
@@ -48,13 +59,22 @@ def test_graph_replays_equal_eager_calls(backend):
 
     rng = np.random.default_rng(15)
 
-    def new_inputs():
+    def new_inputs(rep):
         dq8.upload(rng.standard_normal(4 * H * d).astype(np.float32))
         dqf.upload(rng.standard_normal(9 * 64).astype(np.float32))
         dx.upload(rng.standard_normal(2 * 96).astype(np.float32))
+        # the sequences grow by 3 positions a step up to their written length
+        lens["now"] = np.maximum(1, pb.kv_len - 3 * (5 - rep)).astype(np.int32)
+        dl.upload(lens["now"])
 
-    new_inputs()
+    # a capture that passes host lengths is refused (its replays would keep their sizing)
+    with pytest.raises(GlaError, match="captured"):
+        be.capture(lambda: be.decode(p.pool, dq8, o8[1], ds, dl, 4, capacity, H, 0.088, 30.0, page_table=dt,
+                                     page_table_stride=pb.table.shape[1], kv_start_host=pb.kv_start,
+                                     kv_len_host=pb.kv_len))
+    new_inputs(0)
     calls(0)  # sizes the scratch: nothing allocates during the capture
+    calls(1)
     be.sync()
     g = be.capture(lambda: calls(1))
     big = be.create_q8_weights(orc.q8_quantize_rows(synth.normal_rows(16, 512, 4096)).reshape(-1), 512, 4096)
@@ -65,7 +85,7 @@ def test_graph_replays_equal_eager_calls(backend):
                 be.matvec_q8_0(big, bx, 64, by)
                 be.sync()
                 assert np.isfinite(by.download((64 * 512,))).all()
-            new_inputs()
+            new_inputs(rep)
             calls(0)
             g.replay()
             be.sync()

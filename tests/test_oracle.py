@@ -179,6 +179,31 @@ def test_softcap_vs_f64():
     check_softcap_f64(orc.lib())
 
 
+def test_softcap_known_answers():
+    """The reference's soft-cap known answers (src/tensor/ops.rs:457-471, cap 50: 0 -> 0,
+    +-50 -> +-50 tanh(1), +-1000 -> +-50) through flash_attn_1d_ext: two positions a, b with
+    scores s_a, s_b (q = e_0, k = s e_0, scale 1), V_a = 0 and V_b = M e_1, so out[1] =
+    M / (1 + exp(cap(s_a) - cap(s_b))) with the known capped values; M makes out[1] ~0.1, so
+    a capped score off by 1e-4 moves out[1] by 1e-4 relative, and an uncapped 1000 sends it to
+    0. (The GPU kernels are checked on the same construction.)"""
+    d = 64
+    known = {0.0: 0.0, 5.0: 50.0 * np.tanh(0.1), 50.0: 50.0 * np.tanh(1.0), -50.0: -50.0 * np.tanh(1.0),
+             1000.0: 50.0, -1000.0: -50.0}
+    for sa, sb in [(1000.0, 50.0), (-50.0, -1000.0), (0.0, 5.0), (-1000.0, 1000.0)]:
+        k = np.zeros((1, 2, d), np.float32)
+        v = np.zeros_like(k)
+        k[0, 0, 0], k[0, 1, 0] = sa, sb
+        ratio = np.exp(known[sa] - known[sb])
+        M = min(1e4, 0.1 * (1.0 + ratio))
+        v[0, 1, 1] = M
+        st = orc.kv_cache(k, v)
+        got = orc.flash_attn_1d_ext(np.eye(d, dtype=np.float32)[0], st, 0, 0, 0, 2, d, 1.0, softcap=50.0)
+        want = M / (1.0 + ratio)
+        assert want > 0.05
+        assert abs(got[1] - want) <= 1e-5 * want, (sa, sb, got[1], want)
+        assert not np.delete(got, 1).any()
+
+
 def test_flash_special_cases():
     rng = np.random.default_rng(13)
     d = 64
