@@ -21,6 +21,7 @@ GLA_ERR_INVALID = -5
 GLA_ERR_POOL_EXHAUSTED = -6
 
 GLA_PAGE_SIZE = 16
+GLA_DECODE_NOALLOC_SCRATCH_BYTES = 16 << 20
 GLA_KV_F32 = 0
 GLA_KV_Q8_0 = 1
 GLA_PREC_F32 = 0
@@ -120,6 +121,7 @@ SIGNATURES = {
     "gla_pool_zero_page": (_I, [_P, _P, _I]),
     "gla_window_start": (_L, [_L, _L, _I, _I]),
     "gla_decode": (_I, [_P, C.POINTER(DecodeArgs)]),
+    "gla_decode_noalloc": (_I, [_P, C.POINTER(DecodeArgs)]),
     "gla_prefill": (_I, [_P, C.POINTER(PrefillArgs)]),
     "gla_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _P]),
     "gla_attention_resident": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),

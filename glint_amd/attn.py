@@ -429,10 +429,12 @@ class GpuBackend:
                kv_len: DeviceBuffer, n_seqs: int, max_kv_len: int, n_heads: int, scale: float,
                softcap: Optional[float] = None, layer: int = 0, seq_slot: Optional[DeviceBuffer] = None,
                page_table: Optional[DeviceBuffer] = None, page_table_stride: int = 0,
-               kv_start_host: Optional[np.ndarray] = None, kv_len_host: Optional[np.ndarray] = None) -> None:
+               kv_start_host: Optional[np.ndarray] = None, kv_len_host: Optional[np.ndarray] = None,
+               noalloc: bool = False) -> None:
         """gla_decode on device buffers (asynchronous on the backend's stream). kv_start_host /
         kv_len_host: optional host copies of the device arrays (int32[B]); they let the library
-        size the launch to the real lengths."""
+        size the launch to the real lengths. noalloc: call gla_decode_noalloc (partials in the
+        library's static per-GPU scratch; nothing is allocated)."""
         a = _lib.DecodeArgs()
         a.kv = kv.handle
         a.layer = layer
@@ -457,7 +459,8 @@ class GpuBackend:
                 raise ValueError("kv_start_host / kv_len_host must be int32[n_seqs]")
             a.kv_start_host = hs.ctypes.data
             a.kv_len_host = hl.ctypes.data
-        check(_lib.lib().gla_decode(self.ctx, C.byref(a)))
+        fn = _lib.lib().gla_decode_noalloc if noalloc else _lib.lib().gla_decode
+        check(fn(self.ctx, C.byref(a)))
 
     def prefill(self, kv: _KvBase, q: DeviceBuffer, out: DeviceBuffer, q_start: DeviceBuffer,
                 pos_offset: DeviceBuffer, n_seqs: int, max_q_len: int, n_heads: int, scale: float,

@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <exception>
+#include <mutex>
 #include <new>
 
 #include "gla_internal.h"
@@ -98,6 +99,41 @@ int ensure_hstage(gla_ctx *ctx, size_t bytes) {
 
 static bool head_dim_ok(int d) { return d == 64 || d == 128 || d == 256; }
 
+// Split partials of gla_decode_noalloc: one array per GPU, held until the
+// process ends. In host code `scratch` is only a stand-in for the symbol;
+// kernels get the device address gla_create resolved for the device.
+static __device__ __align__(256) uint8_t scratch[GLA_DECODE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];
+static hipError_t g_scratch_err[kMaxDevices];
+
+// Resolve `scratch` on `device` (which must be current), once per device.
+static void resolve_scratch(int device) {
+    if (device < 0 || device >= kMaxDevices) return;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device]) return;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch_err[device] = e;
+    if (e == hipSuccess) g_scratch_ptr[device] = ptr;
+}
+
+// The device address of `device`'s array, or NULL with the error set.
+static void *scratch_of(int device) {
+    if (device < 0 || device >= kMaxDevices) {
+        set_error(GLA_ERR_DEVICE, "gla_decode_noalloc: device %d beyond the %d the library tracks", device,
+                  kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device])
+        set_error(GLA_ERR_DEVICE, "gla_decode_noalloc: the static scratch of device %d has no address (%s)", device,
+                  hipGetErrorString(g_scratch_err[device]));
+    return g_scratch_ptr[device];
+}
+
 // Waits for the context's stream when it goes out of scope unless released:
 // a host-pointer entry point that queued a copy out of the pinned staging
 // buffer and then fails must not return while that copy is pending (the
@@ -150,6 +186,7 @@ int gla_create(int device, gla_ctx **out) {
                          e == hipSuccess ? "device count 0" : hipGetErrorString(e));
     GLA_REQUIRE(device >= 0 && device < n, "gla_create: device %d out of range (have %d)", device, n);
     GLA_CHECK_HIP(hipSetDevice(device), GLA_ERR_DEVICE);
+    resolve_scratch(device);  // the static scratch of gla_decode_noalloc
     gla_ctx *ctx = new gla_ctx();
     ctx->device = device;
     if (hipDeviceGetAttribute(&ctx->n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
@@ -508,41 +545,45 @@ static int page_map_of(const gla_kv *kv, int layer, const int32_t *seq_slot, con
     return GLA_OK;
 }
 
-int gla_decode(gla_ctx *ctx, const gla_decode_args *a) {
-    GLA_GUARD_BEGIN
-    GLA_REQUIRE(ctx && a && a->kv, "gla_decode: NULL argument");
+// Validate gla_decode_args and fill the launch; *nothing = true when the
+// batch is empty (GLA_OK, nothing to launch).
+static int decode_launch_of(gla_ctx *ctx, const gla_decode_args *a, const char *fn, DecodeLaunch *d,
+                            bool *nothing) {
+    *nothing = false;
+    GLA_REQUIRE(ctx && a && a->kv, "%s: NULL argument", fn);
     const gla_kv *kv = a->kv;
-    GLA_REQUIRE(a->n_seqs >= 0, "gla_decode: n_seqs < 0");
-    if (a->n_seqs == 0) return GLA_OK;
-    GLA_REQUIRE(a->q && a->out && a->kv_start && a->kv_len, "gla_decode: NULL buffer");
+    GLA_REQUIRE(a->n_seqs >= 0, "%s: n_seqs < 0", fn);
+    if (a->n_seqs == 0) {
+        *nothing = true;
+        return GLA_OK;
+    }
+    GLA_REQUIRE(a->q && a->out && a->kv_start && a->kv_len, "%s: NULL buffer", fn);
     GLA_REQUIRE(a->n_heads > 0 && a->n_heads % kv->n_kv_heads == 0,
-                "gla_decode: n_heads %d is not a multiple of n_kv_heads %d", a->n_heads, kv->n_kv_heads);
-    GLA_REQUIRE(a->max_kv_len >= 0, "gla_decode: max_kv_len < 0");
+                "%s: n_heads %d is not a multiple of n_kv_heads %d", fn, a->n_heads, kv->n_kv_heads);
+    GLA_REQUIRE(a->max_kv_len >= 0, "%s: max_kv_len < 0", fn);
     GLA_REQUIRE(!kv->is_pool || a->page_table_stride * GLA_PAGE_SIZE >= a->max_kv_len,
-                "gla_decode: page_table_stride %d cannot cover max_kv_len %d", a->page_table_stride,
-                a->max_kv_len);
-    GLA_REQUIRE(kv->is_pool || a->max_kv_len <= kv->max_seq, "gla_decode: max_kv_len %d > cache max_seq %d",
+                "%s: page_table_stride %d cannot cover max_kv_len %d", fn, a->page_table_stride, a->max_kv_len);
+    GLA_REQUIRE(kv->is_pool || a->max_kv_len <= kv->max_seq, "%s: max_kv_len %d > cache max_seq %d", fn,
                 a->max_kv_len, kv->max_seq);
-    DecodeLaunch d;
-    int rc = page_map_of(kv, a->layer, a->seq_slot, a->page_table, a->page_table_stride, &d.pm);
+    int rc = page_map_of(kv, a->layer, a->seq_slot, a->page_table, a->page_table_stride, &d->pm);
     if (rc != GLA_OK) return rc;
-    d.kv = layout_of(kv);
-    d.q8 = kv->dtype == GLA_KV_Q8_0;
-    d.head_dim = kv->head_dim;
-    d.n_kv_heads = kv->n_kv_heads;
-    d.n_seqs = a->n_seqs;
-    d.kv_start = a->kv_start;
-    d.kv_len = a->kv_len;
-    d.max_kv_len = a->max_kv_len;
-    d.n_heads = a->n_heads;
-    d.scale = a->scale;
-    d.softcap = a->softcap;
-    d.q = a->q;
-    d.out = a->out;
+    d->kv = layout_of(kv);
+    d->q8 = kv->dtype == GLA_KV_Q8_0;
+    d->head_dim = kv->head_dim;
+    d->n_kv_heads = kv->n_kv_heads;
+    d->n_seqs = a->n_seqs;
+    d->kv_start = a->kv_start;
+    d->kv_len = a->kv_len;
+    d->max_kv_len = a->max_kv_len;
+    d->n_heads = a->n_heads;
+    d->scale = a->scale;
+    d->softcap = a->softcap;
+    d->q = a->q;
+    d->out = a->out;
     GLA_REQUIRE((a->kv_start_host == nullptr) == (a->kv_len_host == nullptr),
-                "gla_decode: pass both kv_start_host and kv_len_host, or neither");
-    d.kv_start_host = a->kv_start_host;
-    d.kv_len_host = a->kv_len_host;
+                "%s: pass both kv_start_host and kv_len_host, or neither", fn);
+    d->kv_start_host = a->kv_start_host;
+    d->kv_len_host = a->kv_len_host;
     GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
     if (a->kv_len_host) {
         // The host lengths size the launch; a captured graph would replay
@@ -550,9 +591,32 @@ int gla_decode(gla_ctx *ctx, const gla_decode_args *a) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         GLA_CHECK_HIP(hipStreamIsCapturing(ctx->stream, &cs), GLA_ERR_DEVICE);
         GLA_REQUIRE(cs == hipStreamCaptureStatusNone,
-                    "gla_decode: host lengths are not allowed while the stream is being captured (a graph replay "
-                    "would keep the launch sized for them); pass max_kv_len = the capacity and no host lengths");
+                    "%s: host lengths are not allowed while the stream is being captured (a graph replay would "
+                    "keep the launch sized for them); pass max_kv_len = the capacity and no host lengths",
+                    fn);
     }
+    return GLA_OK;
+}
+
+int gla_decode(gla_ctx *ctx, const gla_decode_args *a) {
+    GLA_GUARD_BEGIN
+    DecodeLaunch d;
+    bool nothing = false;
+    int rc = decode_launch_of(ctx, a, "gla_decode", &d, &nothing);
+    if (rc != GLA_OK || nothing) return rc;
+    return launch_decode(ctx, d);
+    GLA_GUARD_END
+}
+
+int gla_decode_noalloc(gla_ctx *ctx, const gla_decode_args *a) {
+    GLA_GUARD_BEGIN
+    DecodeLaunch d;
+    bool nothing = false;
+    int rc = decode_launch_of(ctx, a, "gla_decode_noalloc", &d, &nothing);
+    if (rc != GLA_OK || nothing) return rc;
+    d.scratch = scratch_of(ctx->device);
+    if (!d.scratch) return GLA_ERR_DEVICE;
+    d.scratch_cap = GLA_DECODE_NOALLOC_SCRATCH_BYTES;
     return launch_decode(ctx, d);
     GLA_GUARD_END
 }

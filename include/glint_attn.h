@@ -191,6 +191,23 @@ typedef struct gla_decode_args {
 
 int gla_decode(gla_ctx *ctx, const gla_decode_args *args);
 
+/* Device scratch gla_decode_noalloc may use, in bytes (one array per GPU). */
+#define GLA_DECODE_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* gla_decode that allocates nothing. It has no counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and bit-identical results as gla_decode; the split
+ * partials live in a static device array of GLA_DECODE_NOALLOC_SCRATCH_BYTES
+ * that each GPU the library runs on holds until the process ends (resolved
+ * once per device by gla_create). A call whose partials need more returns
+ * GLA_ERR_INVALID before anything is launched (at Llama-3-8B heads: B=64 at
+ * 8,192 positions needs 5.3 MiB). Every call on one GPU shares that GPU's
+ * array and leaves its partials in it: calls that overlap on one GPU (two
+ * streams or two contexts) race. Nothing in it needs clearing: a call
+ * writes every partial it reads. */
+int gla_decode_noalloc(gla_ctx *ctx, const gla_decode_args *args);
+
 /* Batched causal prefill: query row r of sequence b sits at absolute
  * position pos_offset[b] + (r - q_start[b]) and attends positions
  * [w, that position] of the sequence's KV, w = max(0, pos - sliding_window + 1)
