@@ -9,26 +9,39 @@ at batch 64 (config 3), with every input resident in HBM. The other
 configurations are reported under "secondary": config 1 (SmolLM decode
 latency, eagerly and with its layers' calls replayed as one HIP graph),
 config 2 (32 layers of f32 decode), config 4 (4x2048 causal prefill,
-TFLOP/s), config 5 (Gemma-2 windowed + global decode) and "proj", the Q8_0
-QKV projection matvec beside attention (1 and 64 tokens).
+TFLOP/s, fp32 and bf16-input), config 5 (Gemma-2 windowed + global decode)
+and "proj", the Q8_0 QKV projection matvec beside attention (1 and 64 tokens).
 
-A step is one gla_decode (or gla_prefill) call over the whole batch for one
-layer. W untimed steps, then K steps between two HIP events recorded on the
-library's stream (the stream the kernels run on), with a device
-synchronisation on both sides. Consecutive steps alternate between layers
-whose K/V live in different memory, so the 256 MB Infinity Cache cannot
-serve repeats.
+Timing. A step is one gla_decode (or gla_prefill, or gla_matvec_q8_0) call
+over the whole batch for one layer. W untimed steps, then K steps (at least
+20), each between its own pair of HIP events recorded on the library's stream
+(the stream the kernels run on), with a device synchronisation on both sides
+of the timed region. Every leg reports the median, min, max and mean of the
+per-step times ("timing_us"); rates use the median. Consecutive steps
+alternate between layers whose K/V live in different memory, so the 256 MB
+Infinity Cache cannot serve repeats.
 
 roofline: algorithmic bytes of one call (unique K/V bytes of the attended
-positions, page-table entries, q and out) divided by the call's average
+positions, page-table entries, q and out) divided by the call's median
 duration; the call is decode_q8_mfma_kernel + decode_q8_combine_kernel.
 `traffic` comes from the rocprofv3 request-size counter summary committed in
 profiles/decode_q8_cfg3_pmc.md (calibrated against a page-copy kernel of
 known size, see --calibrate), or is null when that file is absent.
 
-cpu_baseline: the C restatement of Glint's CPU flash path (oracle/) on the
-same inputs, on the host cores, parallel over sequences as Glint's Rayon loop
-(src/transformer/forward.rs:1499-1502), on a bounded sample.
+cpu_baseline: the C restatement of Glint's CPU flash path (oracle/), compiled
+on this host with gcc -O3 -march=native -ffp-contract=off, on the same inputs,
+on a bounded sample: one thread for configs 1 and 2 (Glint's single-sequence
+decode is serial over heads, src/transformer/forward.rs:254-269), otherwise
+parallel over sequences (forward.rs:1499-1502) or query positions
+(forward.rs:927-931) on the cores this process may use, at most 16 (a GPU
+box's CPU share). `cores` is the thread count; `host_cores` what the process
+could see.
+
+errors: the GPU output for the cpu_baseline sample (the same call, after the
+timed region) against the oracle's: max_abs_err; max_rel_err over elements
+with |want| >= 1e-3; frac_of_tolerance = max of err / max(abs_tol, rel_tol *
+|want|) (<= 1 is within the bar: abs 1e-4 / rel 1e-3 for fp32, 3e-2 / 3e-2
+for the bf16-input prefill).
 """
 from __future__ import annotations
 
@@ -36,8 +49,10 @@ import argparse
 import ctypes as C
 import json
 import os
+import platform
 import re
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -68,6 +83,7 @@ class HipEvents:
     def __init__(self):
         self.h = C.CDLL("libamdhip64.so.7")
         self.h.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.h.hipEventDestroy.argtypes = [C.c_void_p]
         self.h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
         self.h.hipEventSynchronize.argtypes = [C.c_void_p]
         self.h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
@@ -76,6 +92,9 @@ class HipEvents:
         e = C.c_void_p()
         assert self.h.hipEventCreate(C.byref(e)) == 0
         return e
+
+    def destroy(self, e) -> None:
+        self.h.hipEventDestroy(e)
 
     def record(self, e, stream: int) -> None:
         assert self.h.hipEventRecord(e, C.c_void_p(stream)) == 0
@@ -87,23 +106,96 @@ class HipEvents:
         return float(ms.value)
 
 
-def time_steps(be: GpuBackend, ev: HipEvents, step, steps: int, warmup: int) -> float:
-    """Mean ms per step over `steps` timed steps."""
+class Timing:
+    """Per-call durations (ms) of the samples of one timed region, and the region's total."""
+
+    def __init__(self, per_ms: list[float], region_ms: float, group: int):
+        self.per = np.asarray(per_ms, np.float64)
+        self.region_ms = region_ms
+        self.group = group
+
+    @property
+    def median_ms(self) -> float:
+        return float(np.median(self.per))
+
+    def summary_us(self) -> dict:
+        us = self.per * 1e3
+        return {"median": round(float(np.median(us)), 2), "min": round(float(us.min()), 2),
+                "max": round(float(us.max()), 2), "mean": round(float(us.mean()), 2), "samples": int(us.size),
+                "calls_per_sample": self.group,
+                "region_mean": round(self.region_ms * 1e3 / (us.size * self.group), 2)}
+
+
+def time_steps(be: GpuBackend, ev: HipEvents, step, samples: int, warmup: int, group: int = 1) -> Timing:
+    """W untimed calls, then `samples` samples of `group` consecutive calls, each sample between
+    its own event pair on the library's stream (device synchronisation on both sides of the
+    timed region); per-call time of a sample = its duration / group. One call per sample for the
+    ~0.1-1 ms steps; a group (one model step's layers) for the few-microsecond ones, where an
+    event pair per call would cost as much as the call and leave the GPU waiting on the host."""
     for i in range(warmup):
         step(i)
     be.sync()
-    e0, e1 = ev.create(), ev.create()
-    ev.record(e0, be.stream)
-    for i in range(steps):
-        step(warmup + i)
-    ev.record(e1, be.stream)
+    pairs = [(ev.create(), ev.create()) for _ in range(samples)]
+    n = warmup
+    for a, b in pairs:
+        ev.record(a, be.stream)
+        for _ in range(group):
+            step(n)
+            n += 1
+        ev.record(b, be.stream)
     be.sync()
-    return ev.elapsed_ms(e0, e1) / steps
+    per = [ev.elapsed_ms(a, b) / group for a, b in pairs]
+    region = ev.elapsed_ms(pairs[0][0], pairs[-1][1])
+    for a, b in pairs:
+        ev.destroy(a)
+        ev.destroy(b)
+    return Timing(per, region, group)
 
 
-def cpu_threads() -> int:
-    """Host threads for the CPU baseline: the box's cores, at most 16 (the share of one GPU)."""
-    return max(1, min(16, os.cpu_count() or 1))
+def error_figures(got, want, abs_tol: float, rel_tol: float) -> dict:
+    """The GPU output of a sample against the oracle's (definitions in the module docstring)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    big = np.abs(want) >= 1e-3
+    rel = float((err[big] / np.abs(want[big])).max()) if big.any() else 0.0
+    bar = float((err / np.maximum(abs_tol, rel_tol * np.abs(want))).max())
+    return {"max_abs_err": float(f"{err.max():.3g}"), "max_rel_err": float(f"{rel:.3g}"),
+            "frac_of_tolerance": round(bar, 4), "tolerance": f"abs {abs_tol:g} / rel {rel_tol:g}",
+            "elements": int(err.size)}
+
+
+class CpuBaseline:
+    """The oracle built for this host (oracle.build_native), its thread count and a host
+    description; falls back to the prebuilt portable oracle when gcc fails."""
+
+    def __init__(self):
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as orc
+        self.orc = orc
+        try:
+            self.L = orc.build_native(Path(tempfile.mkdtemp(prefix="glint_oracle_")))
+            self.build = "gcc " + " ".join(orc.NATIVE_FLAGS)
+        except Exception as ex:  # noqa: BLE001 -- the portable build is the fallback
+            self.L = orc.lib()
+            self.build = f"prebuilt oracle/liboracle.so (-O2 -march=x86-64-v3; native build failed: {ex})"
+        self.host_cores = orc.host_cores()
+        self.threads = orc.threads()
+        self.cpu = cpu_model()
+
+    def describe(self, d: dict, threads: int) -> dict:
+        d.update(cores=threads, host_cores=self.host_cores, cpu=self.cpu, build=self.build)
+        return d
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
 
 
 def q8_token_bytes(n_kv: int, d: int) -> int:
@@ -197,27 +289,35 @@ class PagedDecode:
     def bytes_per_step(self):
         return float(np.mean([L["bytes"] for L in self.layers]))
 
-    def cpu_baseline(self, min_seconds=10.0, max_reps=50):
-        sys.path.insert(0, str(ROOT / "oracle"))
-        import oracle as orc
+    def cpu_baseline(self, cb: CpuBaseline, min_seconds=10.0, max_reps=50):
+        """Layer 0 of every sequence through the oracle's decode_batch, one task per sequence.
+        Returns (baseline, the oracle's output [B][H][d])."""
+        orc = cb.orc
         kq, vq, pb = self.host_q8
         pk = kq.reshape(-1, PAGE, kq.shape[-1])
         pv = vq.reshape(-1, PAGE, vq.shape[-1])
-        stores = [orc.paged_q8(pk, pv, self.kv_dim, pb.table[b:b + 1]) for b in range(len(self.ctx))]
+        stores = [orc.paged_q8(pk, pv, self.kv_dim, pb.table[b:b + 1], L=cb.L) for b in range(len(self.ctx))]
         L0 = self.layers[0]
         q = L0["q_host"].reshape(len(self.ctx), -1)
-        nt = cpu_threads()
+        nt = cb.threads
         reps, t0 = 0, time.perf_counter()
         while True:
-            orc.decode_batch(q, stores, 0, pb.kv_start, pb.kv_len, self.H, self.Hkv, self.d, self.scale,
-                             self.softcap, n_threads=nt)
+            out = orc.decode_batch(q, stores, 0, pb.kv_start, pb.kv_len, self.H, self.Hkv, self.d, self.scale,
+                                   self.softcap, n_threads=nt)
             reps += 1
             el = time.perf_counter() - t0
             if el >= min_seconds or reps >= max_reps:
                 break
-        return dict(value=round(L0["bytes"] * reps / el / 1e9, 3), unit="GB/s", cores=nt, kind="port",
+        base = dict(value=round(L0["bytes"] * reps / el / 1e9, 3), unit="GB/s", kind="port",
                     sample=f"{reps} x layer 0 of {self.name} (all {len(self.ctx)} sequences, same inputs), "
-                           f"{el:.1f} s; oracle/glint_oracle.c decode_batch, one thread per sequence")
+                           f"{el:.1f} s; oracle decode_batch, one task per sequence")
+        return cb.describe(base, nt), out.reshape(len(self.ctx), self.H, self.d)
+
+    def gpu_sample(self):
+        """The GPU output of layer 0 (the cpu_baseline sample)."""
+        self.step(0)
+        self.be.sync()
+        return self.layers[0]["out"].download((len(self.ctx), self.H, self.d))
 
 
 class ContigDecode:
@@ -254,22 +354,29 @@ class ContigDecode:
     def bytes_per_step(self):
         return float(2 * self.ctx * self.kv_dim * 4 + 2 * self.H * self.d * 4)
 
-    def cpu_baseline(self, min_seconds=3.0, max_reps=2000):
-        sys.path.insert(0, str(ROOT / "oracle"))
-        import oracle as orc
+    def cpu_baseline(self, cb: CpuBaseline, min_seconds=3.0, max_reps=2000):
+        """Layer 0 through attn_heads_cpu, one thread (Glint's single-sequence decode is serial
+        over heads). Returns (baseline, the oracle's output [1][H][d])."""
+        orc = cb.orc
         k, v = self.host
-        st = orc.kv_cache(k[None], v[None])
+        st = orc.kv_cache(k[None], v[None], L=cb.L)
         q = self.q_host[0].reshape(-1)
         reps, t0 = 0, time.perf_counter()
         while True:
-            orc.attn_heads_cpu(q, st, 0, 0, self.ctx, self.H, self.H // self.Hkv, self.d, self.scale)
+            out = orc.attn_heads_cpu(q, st, 0, 0, self.ctx, self.H, self.H // self.Hkv, self.d, self.scale)
             reps += 1
             el = time.perf_counter() - t0
             if el >= min_seconds or reps >= max_reps:
                 break
-        return dict(value=round(self.bytes_per_step() * reps / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
+        base = dict(value=round(self.bytes_per_step() * reps / el / 1e9, 3), unit="GB/s", kind="port",
                     sample=f"{reps} x layer 0 of {self.name} (attn_heads_cpu, serial over heads as Glint), "
                            f"{el:.1f} s", us_per_layer=round(el / reps * 1e6, 2))
+        return cb.describe(base, 1), out.reshape(1, self.H, self.d)
+
+    def gpu_sample(self):
+        self.step(0)
+        self.be.sync()
+        return self.out.download((1, self.H, self.d))
 
 
 class Prefill:
@@ -309,26 +416,32 @@ class Prefill:
     def flops_per_step(self):
         return float(4 * self.B * self.H * self.d * self.S * (self.S + 1) // 2)
 
-    def cpu_baseline(self, min_seconds=5.0, max_reps=20):
+    def cpu_baseline(self, cb: CpuBaseline, min_seconds=5.0, max_reps=20):
         """Prompt 0 of layer 0 through the oracle's prefill, one task per query position on the
-        host cores as forward.rs:927-931."""
-        sys.path.insert(0, str(ROOT / "oracle"))
-        import oracle as orc
+        host cores as forward.rs:927-931. Returns (baseline, the oracle's output [S][H][d])."""
+        orc = cb.orc
         k, v = self.host
-        st = orc.kv_cache(k[None], v[None])
+        st = orc.kv_cache(k[None], v[None], L=cb.L)
         q = self.q0_host[:self.S].reshape(self.S, -1)
-        nt = cpu_threads()
+        nt = cb.threads
         reps, t0 = 0, time.perf_counter()
         while True:
-            orc.prefill(q, st, 0, 0, self.H, self.Hkv, self.d, self.scale, n_threads=nt)
+            out = orc.prefill(q, st, 0, 0, self.H, self.Hkv, self.d, self.scale, n_threads=nt)
             reps += 1
             el = time.perf_counter() - t0
             if el >= min_seconds or reps >= max_reps:
                 break
         flops = 4 * self.H * self.d * self.S * (self.S + 1) // 2 * reps
-        return dict(value=round(flops / el / 1e12, 6), unit="TFLOP/s", cores=nt, kind="port",
+        base = dict(value=round(flops / el / 1e12, 6), unit="TFLOP/s", kind="port",
                     sample=f"{reps} x prompt 0 of layer 0 ({self.S} positions, causal), oracle prefill, one task "
                            f"per query position, {el:.1f} s")
+        return cb.describe(base, nt), out.reshape(self.S, self.H, self.d)
+
+    def gpu_sample(self):
+        """Prompt 0 of layer 0 at the current precision."""
+        self.step(0)
+        self.be.sync()
+        return self.out.download((self.B * self.S, self.H, self.d))[:self.S]
 
 
 class ProjMatvec:
@@ -361,22 +474,28 @@ class ProjMatvec:
     def bytes_per_step(self):
         return float(self.rows * self.cols // 32 * 34 + self.n_vec * (self.cols + self.rows) * 4)
 
-    def cpu_baseline(self, min_seconds=3.0, max_reps=50):
+    def cpu_baseline(self, cb: CpuBaseline, min_seconds=3.0, max_reps=50):
         """One layer's QKV matvec for one token through the oracle's restatement of
-        matvec_q8_0_scalar (quantized.rs:587-610), one thread."""
-        sys.path.insert(0, str(ROOT / "oracle"))
-        import oracle as orc
+        matvec_q8_0_scalar (quantized.rs:587-610), one thread. Returns (baseline, y [rows])."""
+        orc = cb.orc
         reps, t0 = 0, time.perf_counter()
         while True:
-            orc.matvec_q8_0(self.raw0, self.rows, self.cols, self.x_host[0])
+            out = orc.matvec_q8_0(self.raw0, self.rows, self.cols, self.x_host[0], L=cb.L)
             reps += 1
             el = time.perf_counter() - t0
             if el >= min_seconds or reps >= max_reps:
                 break
         nbytes = self.rows * self.cols // 32 * 34 * reps
-        return dict(value=round(nbytes / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
+        base = dict(value=round(nbytes / el / 1e9, 3), unit="GB/s", kind="port",
                     sample=f"{reps} x one token through layer 0's 6144 x 4096 weights, oracle matvec_q8_0 "
                            f"(scalar), {el:.1f} s")
+        return cb.describe(base, 1), out
+
+    def gpu_sample(self):
+        """Token 0 through layer 0's weights."""
+        self.step(0)
+        self.be.sync()
+        return self.y.download((self.n_vec, self.rows))[0]
 
 
 def calibrate(be: GpuBackend, n_copies: int = 2048) -> dict:
@@ -428,7 +547,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="all", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "proj", "all"])
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs and the error figures")
     ap.add_argument("--calibrate", action="store_true", help="also run known-size page copies (for PMC runs)")
     ap.add_argument("--achievable", action="store_true",
                     help="measure the achievable ceilings also when one workload is selected")
@@ -441,9 +560,11 @@ def main() -> int:
 
     be = GpuBackend(0)
     ev = HipEvents()
+    cb = None if args.no_cpu else CpuBaseline()
+    steps = max(20, args.steps)  # every leg: the median of at least 20 timed steps
     want = {args.workload} if args.workload != "all" else {"cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "proj"}
     result = {
-        "metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32 (Q8_0 KV; products as exact f16 pieces on MFMA, f32 accumulate and softmax)",
         "data": "synthetic (seeded Xorshift64 + Box-Muller, N(0,1) Q/K/V; K x3 for config 5)",
@@ -458,10 +579,19 @@ def main() -> int:
     def frac_of(value, key):
         return round(value / ach[key], 4) if ach else None
 
+    def baseline_and_errors(wl, entry: dict, tol=(1e-4, 1e-3), **kw):
+        """cpu_baseline on the sample, then the GPU's output for it against the oracle's."""
+        if cb is None:
+            return None
+        base, ref = wl.cpu_baseline(cb, **kw)
+        entry["errors"] = error_figures(wl.gpu_sample(), ref, *tol)
+        return base, ref
+
     if "cfg3" in want:
         log("cfg3: paged Q8_0 pool, 2 layers, B=64")
         wl = PagedDecode(be, "cfg3", 32, 8, 128, 64, 128, 8192, 256, None, [None, None], 1.0, SEED + 3)
-        ms = time_steps(be, ev, wl.step, args.steps, args.warmup)
+        t = time_steps(be, ev, wl.step, steps, args.warmup)
+        ms = t.median_ms
         gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
         traffic, src = traffic_from_profile()
         result.update(value=round(gbs, 2), ms_per_step=round(ms, 5))
@@ -480,106 +610,121 @@ def main() -> int:
             "frac_of_achievable": frac_of(gbs, "hbm_read_gbs"),
             "kernel": "decode_q8_mfma_kernel<128> + decode_q8_combine_kernel<128> (one gla_decode call)",
             "algorithmic_bytes_per_call": int(wl.bytes_per_step()),
-            "us_per_call": round(ms * 1e3, 2),
+            "us_per_call": round(ms * 1e3, 2), "timing_us": t.summary_us(),
         }
         if src:
             result["roofline"]["traffic_source"] = src
-        log(f"cfg3: {ms * 1e3:.1f} us/call, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of peak)")
-        if not args.no_cpu:
-            log("cfg3: CPU baseline (oracle, same inputs)")
-            result["cpu_baseline"] = wl.cpu_baseline()
+        log(f"cfg3: {ms * 1e3:.1f} us/call (median; min {t.per.min() * 1e3:.1f}, max {t.per.max() * 1e3:.1f}), "
+            f"{gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of peak)")
+        if cb:
+            log("cfg3: CPU baseline and errors (oracle, same inputs)")
+            errs = {}
+            result["cpu_baseline"], _ = baseline_and_errors(wl, errs)
+            result["errors"] = errs["errors"]
         del wl
     if "cfg5" in want:
         log("cfg5: Gemma-2 paged Q8_0 pool (windowed + global layer)")
         wl = PagedDecode(be, "cfg5", 16, 8, 256, 32, 2048, 8192, 0, 50.0, [4096, None], 3.0, SEED + 5)
-        ms = time_steps(be, ev, wl.step, args.steps, args.warmup)
+        t = time_steps(be, ev, wl.step, steps, args.warmup)
+        ms = t.median_ms
         gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
-        secondary["cfg5"] = {
+        e = secondary["cfg5"] = {
             "workload": "Gemma-2-9B decode, paged Q8_0, B=32, ctx U[2048,8192], soft-cap 50, window 4096 and "
                         "global layers alternating (one step = one layer)",
-            "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
+            "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2), "timing_us": t.summary_us(),
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs")}
-        if not args.no_cpu:
-            secondary["cfg5"]["cpu_baseline"] = wl.cpu_baseline(min_seconds=5.0, max_reps=10)
+        if cb:
+            e["cpu_baseline"], _ = baseline_and_errors(wl, e, min_seconds=5.0, max_reps=10)
         log(f"cfg5: {ms * 1e3:.1f} us/layer, {gbs:.1f} GB/s")
         del wl
     if "cfg2" in want:
         log("cfg2: 32-layer f32 cache")
         wl = ContigDecode(be, 32, 4096, 32, 8, 128, 0x2222, "cfg2")
-        ms = time_steps(be, ev, wl.step, max(args.steps, 64), args.warmup)
+        t = time_steps(be, ev, wl.step, steps, args.warmup, group=wl.n_layers)
+        ms = t.median_ms
         gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
-        secondary["cfg2"] = {
+        e = secondary["cfg2"] = {
             "workload": "Llama-3-8B single-sequence decode, f32 contiguous ctx 4096, 32 layers back to back",
-            "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
+            "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2), "timing_us": t.summary_us(),
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs")}
-        if not args.no_cpu:
-            secondary["cfg2"]["cpu_baseline"] = wl.cpu_baseline()
+        if cb:
+            e["cpu_baseline"], _ = baseline_and_errors(wl, e)
         log(f"cfg2: {ms * 1e3:.1f} us/layer, {gbs:.1f} GB/s")
         del wl
     if "cfg1" in want:
         log("cfg1: SmolLM-135M decode, f32 ctx 512")
         wl = ContigDecode(be, 8, 512, 9, 3, 64, 0x1111, "cfg1")
-        ms = time_steps(be, ev, wl.step, max(args.steps, 64), args.warmup)
-        secondary["cfg1"] = {
+        t = time_steps(be, ev, wl.step, steps, args.warmup, group=wl.n_layers)
+        ms = t.median_ms
+        e = secondary["cfg1"] = {
             "workload": "SmolLM-135M decode, H9/KV3 d64, B=1, f32 contiguous ctx 512 (latency)",
-            "value": round(ms * 1e3, 2), "unit": "us/call",
+            "value": round(ms * 1e3, 2), "unit": "us/call", "timing_us": t.summary_us(),
             "GB_per_s": round(wl.bytes_per_step() / (ms * 1e-3) / 1e9, 2)}
-        if not args.no_cpu:
-            secondary["cfg1"]["cpu_baseline"] = wl.cpu_baseline(min_seconds=2.0, max_reps=20000)
+        if cb:
+            e["cpu_baseline"], _ = baseline_and_errors(wl, e, min_seconds=2.0, max_reps=20000)
         log(f"cfg1: {ms * 1e3:.2f} us/call")
         # the same layers' calls captured as one HIP graph (a decode step's attention), replayed:
         # the launch cost of a call is then paid once per step, not once per kernel
         g = be.capture(lambda: [wl.step(i) for i in range(wl.n_layers)])
-        ms_g = time_steps(be, ev, lambda i: g.replay(), max(args.steps, 64), args.warmup) / wl.n_layers
+        t = time_steps(be, ev, lambda i: g.replay(), steps, args.warmup, group=4)
+        ms_g = t.median_ms / wl.n_layers
         g.destroy()
         secondary["cfg1_graph"] = {
             "workload": f"cfg1, the {wl.n_layers} layers' gla_decode calls captured as one HIP graph and replayed",
-            "value": round(ms_g * 1e3, 2), "unit": "us/call",
+            "value": round(ms_g * 1e3, 2), "unit": "us/call", "timing_us_per_replay": t.summary_us(),
             "GB_per_s": round(wl.bytes_per_step() / (ms_g * 1e-3) / 1e9, 2)}
         log(f"cfg1 graph: {ms_g * 1e3:.2f} us/call")
         del wl
     if "cfg4" in want:
         log("cfg4: 4x2048 causal prefill, f32 KV cache")
         wl = Prefill(be)
-        ms = time_steps(be, ev, wl.step, max(3, args.steps // 5), min(args.warmup, 2))
+        t = time_steps(be, ev, wl.step, steps, args.warmup)
+        ms = t.median_ms
         tf = wl.flops_per_step() / (ms * 1e-3) / 1e12
-        secondary["cfg4_f32"] = {
+        e = secondary["cfg4_f32"] = {
             "workload": "Llama-3-8B causal prefill 4x2048, f32 KV cache, fp32-input MFMA",
-            "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+            "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "timing_us": t.summary_us(),
             "frac_of_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
             "frac_of_achievable_fp32_mfma": frac_of(tf, "fp32_mfma_tflops")}
-        if not args.no_cpu:
-            secondary["cfg4_f32"]["cpu_baseline"] = wl.cpu_baseline()
+        ref = None
+        if cb:
+            e["cpu_baseline"], ref = baseline_and_errors(wl, e)
         log(f"cfg4 f32: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
         # bf16-input variant: same inputs rounded to bf16 inside the kernel
         wl.precision = "bf16"
-        ms = time_steps(be, ev, wl.step, max(3, args.steps // 5), min(args.warmup, 2))
+        t = time_steps(be, ev, wl.step, steps, args.warmup)
+        ms = t.median_ms
         tf = wl.flops_per_step() / (ms * 1e-3) / 1e12
-        secondary["cfg4_bf16"] = {
+        e = secondary["cfg4_bf16"] = {
             "workload": "Llama-3-8B causal prefill 4x2048, f32 KV cache, bf16-input MFMA (fp32 accumulate)",
-            "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+            "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "timing_us": t.summary_us(),
             "frac_of_bf16_mfma_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
             "frac_of_achievable_bf16_mfma": frac_of(tf, "bf16_mfma_tflops"),
             "tolerance": "max abs 3e-2 / rel 3e-2 vs the fp32 oracle (tests/test_gpu_prefill.py)"}
+        if ref is not None:
+            e["errors"] = error_figures(wl.gpu_sample(), ref, 3e-2, 3e-2)
         log(f"cfg4 bf16: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
         del wl
     if "proj" in want:
         for n_vec in (1, 64):
             log(f"proj: Q8_0 QKV matvec, {n_vec} token(s)")
             wl = ProjMatvec(be, n_vec)
-            ms = time_steps(be, ev, wl.step, max(args.steps, 50), args.warmup)
+            t = time_steps(be, ev, wl.step, steps, args.warmup, group=len(wl.w))
+            ms = t.median_ms
             gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
             key = f"proj_qkv_b{n_vec}"
-            secondary[key] = {
+            e = secondary[key] = {
                 "workload": f"Llama-3-8B fused QKV projection, 6144 x 4096 GGML Q8_0 weights (16 layers in "
                             f"rotation), {n_vec} token(s) per call (gla_matvec_q8_0)",
                 "value": round(gbs, 2), "unit": "GB/s", "us_per_call": round(ms * 1e3, 2),
-                "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                "timing_us": t.summary_us(), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                 "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs")}
-            if not args.no_cpu and n_vec == 1:
-                secondary[key]["cpu_baseline"] = wl.cpu_baseline()
+            if cb:
+                base = baseline_and_errors(wl, e)
+                if n_vec == 1:
+                    e["cpu_baseline"] = base[0]
             log(f"{key}: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s")
             for w in wl.w:
                 w.destroy()

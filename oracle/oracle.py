@@ -79,8 +79,31 @@ def build_mutant(n: int, out_dir: Path) -> C.CDLL:
     return _bind(so)
 
 
+NATIVE_FLAGS = ["-O3", "-march=native", "-ffp-contract=off", "-fno-fast-math"]
+
+
+def build_native(out_dir: Path) -> C.CDLL:
+    """Compile the oracle for the CPU it runs on (gcc -O3 -march=native -ffp-contract=off, no
+    fast-math: the CPU-baseline build; the float operations and their order are those of the
+    portable -O2 build, since gcc does not reassociate without fast-math) and bind it."""
+    out_dir.mkdir(parents=True, exist_ok=True)
+    so = out_dir / "liboracle_native.so"
+    subprocess.run(["gcc", *NATIVE_FLAGS, "-fPIC", "-shared", "-std=c11", "-o", str(so),
+                    str(HERE / "glint_oracle.c"), "-lm", "-pthread"], check=True, capture_output=True)
+    return _bind(so)
+
+
+def host_cores() -> int:
+    """Cores this process may run on (its affinity mask; os.cpu_count() without one)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
 def threads() -> int:
-    return max(1, min(16, os.cpu_count() or 1))
+    """Worker threads: the cores this process may use, at most 16 (a GPU box's CPU share)."""
+    return max(1, min(16, host_cores()))
 
 
 def _p(a: np.ndarray) -> C.c_void_p:
