@@ -44,7 +44,7 @@ struct DecodeParams {
     const float *q;
     float *out;
     float *part_acc;  // [unit][split][GT][D]
-    float *part_ml;   // [unit][split][GT][2]
+    float *part_ml;   // [unit][split] one 128-byte line: m[GT] at 0, l[GT] at 8, zeros
     int n_heads;
     int n_kv_heads;
     int group;  // n_heads / n_kv_heads
@@ -368,11 +368,33 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
         } else {
             const int64_t slot = unit * p.max_splits + split;
             p.part_acc[(slot * GT + g) * D + e] = A;
-            if (e == 0) {
-                p.part_ml[(slot * GT + g) * 2 + 0] = M;
-                p.part_ml[(slot * GT + g) * 2 + 1] = L;
+        }
+    }
+    // (m, l) of the split's heads as one whole 128-byte line: sub-line writes cost a
+    // read-modify-write in HBM (measured on the Q8_0 kernel's partials: 3-12 us per call)
+    if (r.n_splits > 1 && tid < 8) {
+        float M = -INFINITY, L = 0.0f;
+        const int g = tid & 7;
+        if (g < GT) {
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) M = fmaxf(M, lds_m[w][g]);
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) {
+                const float mw = lds_m[w][g];
+                const float f = (mw == -INFINITY) ? 0.0f : fast_exp2(mw - M);
+                L = fmaf(lds_l[w][g], f, L);
             }
         }
+        // lane t < 4 writes floats 4t .. 4t+3 of the line: m[0..7], l[0..7]; lanes 4..7 zeros
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int src = (4 * tid + j) & 7;  // the head whose m (tid < 2) or l (tid 2, 3) goes here
+            const float m_s = __shfl(M, src), l_s = __shfl(L, src);
+            v[j] = tid < 2 ? m_s : (tid < 4 ? l_s : 0.0f);
+        }
+        const int64_t slot = unit * p.max_splits + split;
+        *reinterpret_cast<float4 *>(p.part_ml + slot * 32 + 4 * tid) = make_float4(v[0], v[1], v[2], v[3]);
     }
 }
 
@@ -411,8 +433,8 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(const DecodePa
             const int s = s0 + j * NSG;
             const int sc = s < r.n_splits ? s : s0;
             const int64_t slot = (slot0 + sc) * GT + g;
-            mi[j] = s < r.n_splits ? p.part_ml[slot * 2] : -INFINITY;
-            li[j] = p.part_ml[slot * 2 + 1];
+            mi[j] = s < r.n_splits ? p.part_ml[(slot0 + sc) * 32 + g] : -INFINITY;
+            li[j] = p.part_ml[(slot0 + sc) * 32 + 8 + g];
             ai[j] = reinterpret_cast<const float4 *>(p.part_acc + slot * D)[e4];
         }
         float bm = M;
@@ -558,7 +580,7 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
     if (max_splits > 1) {
         const size_t slots = (size_t)units * max_splits;
         const size_t acc_b = slots * gt * D * sizeof(float);
-        const size_t ml_b = slots * gt * 2 * sizeof(float);
+        const size_t ml_b = slots * 32 * sizeof(float);
         void *scr = nullptr;
         int rc = decode_scratch(ctx, d, acc_b + ml_b, &scr);
         if (rc != GLA_OK) return rc;

@@ -71,6 +71,9 @@ constexpr int kMaxChunks = 64;  // preferred bound on chunks per unit
 // Workgroup rows listed in the launch arguments (see Q8Params::rows): 3 KB of
 // the 4 KB kernel-argument limit.
 constexpr int kMaxRows = 1536;
+// Floats per (unit, workgroup) partial: O, then one 128-byte line holding m and l.
+template <int D>
+constexpr int kPartStride = kGT * D + 32;
 
 struct Q8Params {
     const uint8_t *base;  // KV storage; a (page, head) block is 34*D bytes
@@ -81,7 +84,7 @@ struct Q8Params {
     const int32_t *kv_len;
     const float *q;
     float *out;
-    float *part;  // [unit][max_wg][kGT][D + 2]: O (unnormalised), m, l
+    float *part;  // [unit][max_wg] { O[kGT][D] (unnormalised) | m[kGT], l[kGT], zeros: 32 floats }
     int n_heads;
     int n_kv_heads;
     int group;
@@ -708,34 +711,18 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
     }
 }
 
-// Grid (workgroup split, KV head x head group, sequence); the 4 waves of a
-// workgroup take 4 consecutive chunks of the unit and merge them in LDS. A
+// One workgroup item: (sequence b, its workgroup wg, KV head x head group hx).
+// The 4 waves take 4 consecutive chunks of the unit and merge them in LDS; a
 // unit longer than one workgroup writes one partial per workgroup.
 template <int D>
-__global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Params p) {
-    // per wave: the streaming slot, later the wave's [kGT][D + 2] result
-    __shared__ __attribute__((aligned(16))) uint8_t slots[kWaves][kSlotBytesPerD * D];
-    static_assert(kGT * (D + 2) * 4 <= kSlotBytesPerD * D, "the merge result fits in the slot");
+__device__ __forceinline__ void q8_item(const Q8Params &p, uint8_t (*slots)[kSlotBytesPerD * D], int b, int wg,
+                                        int hx) {
     constexpr int kThreads = kWaves * 64;
-
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    // grid (KV head x head group, workgroup of the sequence, sequence): the
-    // head index runs fastest, so the workgroups reading the 8 head spans of
-    // the same pages are dispatched together and the DRAM rows those pages
-    // open are read out while open (measured ~25% over chunk-fastest order)
-    int b, wg;
-    if (p.n_rows > 0) {
-        const int e = p.rows[blockIdx.y];
-        b = e >> 6;
-        wg = e & 63;
-    } else {
-        b = blockIdx.z;
-        wg = blockIdx.y;
-    }
-    const int kvh = blockIdx.x / p.n_hg;
-    const int hg = blockIdx.x - kvh * p.n_hg;
+    const int kvh = hx / p.n_hg;
+    const int hg = hx - kvh * p.n_hg;
     const int g0 = hg * p.hpw;
     const int gcount = min(p.hpw, p.group - g0);
     const int h_base = kvh * p.group + g0;
@@ -773,40 +760,87 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
         return reinterpret_cast<const float *>(slots[w])[g * (D + 2) + i];
     };
 
-    // merge the workgroup's waves; thread -> (head g, element d)
+    // merge the workgroup's waves; thread -> (head g, elements d .. d+3)
     const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
-    const int64_t pstride = (int64_t)kGT * (D + 2);  // floats per (unit, workgroup) partial
-    float *mine = p.part + (unit * p.max_wg + wg) * pstride;
-    for (int idx = tid; idx < kGT * D; idx += kThreads) {
-        const int g = idx / D;
-        const int d = idx - g * D;
+    float *mine = p.part + (unit * p.max_wg + wg) * kPartStride<D>;
+    float Mg = -INFINITY, Lg = 0.0f;  // (M, L) of head tid, for the (m, l) line
+    if (tid < kGT) {
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) Mg = fmaxf(Mg, res(w, tid, D));
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            const float mw = res(w, tid, D);
+            if (mw != -INFINITY) Lg = fmaf(res(w, tid, D + 1), fast_exp2(mw - Mg), Lg);
+        }
+    }
+    for (int i4 = tid; i4 < kGT * D / 4; i4 += kThreads) {
+        const int g = (4 * i4) / D;
+        const int d = 4 * i4 - g * D;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kWaves; w++) M = fmaxf(M, res(w, g, D));
-        float L = 0.0f, A = 0.0f;
+        float L = 0.0f;
+        float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int w = 0; w < kWaves; w++) {
             const float mw = res(w, g, D);
             if (mw != -INFINITY) {
                 const float f = fast_exp2(mw - M);
                 L = fmaf(res(w, g, D + 1), f, L);
-                A = fmaf(res(w, g, d), f, A);
+                A.x = fmaf(res(w, g, d + 0), f, A.x);
+                A.y = fmaf(res(w, g, d + 1), f, A.y);
+                A.z = fmaf(res(w, g, d + 2), f, A.z);
+                A.w = fmaf(res(w, g, d + 3), f, A.w);
             }
         }
         if (n_wg == 1) {
-            if (g < gcount) out[g * D + d] = L > 0.0f ? A * (1.0f / L) : 0.0f;
+            const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+            if (g < gcount)
+                *reinterpret_cast<float4 *>(out + g * D + d) = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
         } else {
-            mine[g * (D + 2) + d] = A;
-            if (d == 0) {
-                mine[g * (D + 2) + D] = M;
-                mine[g * (D + 2) + D + 1] = L;
-            }
+            *reinterpret_cast<float4 *>(mine + g * D + d) = A;
         }
+    }
+    // The (m, l) of the partial fill one whole 128-byte line: m[kGT], l[kGT], zeros. (Partial
+    // lines, and the partials' rows at a 520-byte stride, measured 3-12 us slower per cfg3 call:
+    // sub-line writes cost a read-modify-write in HBM.)
+    if (n_wg > 1 && tid < 8) {
+        const float Ms = __shfl(Mg, tid & 3), Ls = __shfl(Lg, tid & 3);
+        const float v = tid < kGT ? Ms : Ls;
+        const float a0 = __shfl(v, 0), a1 = __shfl(v, 1), a2 = __shfl(v, 2), a3 = __shfl(v, 3);
+        const float b0 = __shfl(v, 4), b1 = __shfl(v, 5), b2 = __shfl(v, 6), b3 = __shfl(v, 7);
+        float4 line = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (tid == 0) line = make_float4(a0, a1, a2, a3);
+        if (tid == 1) line = make_float4(b0, b1, b2, b3);
+        *reinterpret_cast<float4 *>(mine + kGT * D + 4 * tid) = line;
     }
     // Units with more than one workgroup are merged by decode_q8_combine_kernel.
     // (Merging here in the last workgroup to finish needs a device-scope
     // release per workgroup; on gfx950 that is an L2 writeback each time and
     // measured ~6x slower than the extra launch.)
+}
+
+
+// Grid (KV head x head group, workgroup of the sequence, sequence), or with
+// the host lengths (KV head x head group, row of the longest-first list).
+// The head index runs fastest, so the workgroups reading the 8 head spans of
+// the same pages are dispatched together and the DRAM rows those pages open
+// are read out while open (measured ~25% over chunk-fastest order).
+template <int D>
+__global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Params p) {
+    // per wave: the streaming slot, later the wave's [kGT][D + 2] result
+    __shared__ __attribute__((aligned(16))) uint8_t slots[kWaves][kSlotBytesPerD * D];
+    static_assert(kGT * (D + 2) * 4 <= kSlotBytesPerD * D, "the merge result fits in the slot");
+    int b, wg;
+    if (p.n_rows > 0) {
+        const int e = p.rows[blockIdx.y];
+        b = e >> 6;
+        wg = e & 63;
+    } else {
+        b = blockIdx.z;
+        wg = blockIdx.y;
+    }
+    q8_item<D>(p, slots, b, wg, blockIdx.x);
 }
 
 // Merge of the workgroup partials of every unit with more than one
@@ -828,8 +862,8 @@ __global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p
     const int d = idx - g * D;
     if (g >= gcount) return;
     const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
-    const int64_t pstride = (int64_t)kGT * (D + 2);
-    const float *hp = p.part + unit * p.max_wg * pstride + g * (D + 2);
+    constexpr int64_t pstride = kPartStride<D>;
+    const float *hp = p.part + unit * p.max_wg * pstride;
     // one pass, eight partials at a time: all loads of a batch are in flight
     // together, and (M, L, A) absorb the batch with one rescale
     float M = -INFINITY, L = 0.0f, A = 0.0f;
@@ -838,9 +872,9 @@ __global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int i = min(i0 + j, n_wg - 1);
-            mi[j] = (i0 + j < n_wg) ? hp[i * pstride + D] : -INFINITY;
-            li[j] = hp[i * pstride + D + 1];
-            ai[j] = hp[i * pstride + d];
+            mi[j] = (i0 + j < n_wg) ? hp[i * pstride + kGT * D + g] : -INFINITY;
+            li[j] = hp[i * pstride + kGT * D + kGT + g];
+            ai[j] = hp[i * pstride + g * D + d];
         }
         float bm = M;
 #pragma unroll
@@ -921,7 +955,10 @@ int choose_hpw(int group, int64_t wg_per_hg, int n_kv_heads, int64_t slots) {
         // the next head-group count that lowers the heads per wave (balanced
         // groups: 4 heads go 4 -> 2 + 2 -> 1 + 1 + 1 + 1)
         int h = hpw, m = n_hg;
-        while (h == hpw) h = (group + (++m) - 1) / m;
+        while (h == hpw) {
+            m++;
+            h = (group + m - 1) / m;
+        }
         m = (group + h - 1) / h;
         if (wg_per_hg * n_kv_heads * m > slots) break;
         hpw = h;
@@ -992,7 +1029,7 @@ int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d) {
     if (max_wg > 65535)
         return set_error(GLA_ERR_INVALID, "decode: %lld workgroups per sequence > 65535", (long long)max_wg);
     if (max_wg > 1) {
-        const size_t bytes = (size_t)units * max_wg * kGT * (D + 2) * sizeof(float);
+        const size_t bytes = (size_t)units * max_wg * (kGT * D + 32) * sizeof(float);
         void *scr = nullptr;
         int rc = decode_scratch(ctx, d, bytes, &scr);
         if (rc != GLA_OK) return rc;
