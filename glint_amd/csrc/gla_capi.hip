@@ -210,6 +210,12 @@ int gla_destroy(gla_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     for (const auto &e : ctx->scratch)
         if (e.ptr) (void)hipFree(e.ptr);
+    for (gla_kv *kv : ctx->kvs) {
+        if (kv->base) (void)hipFree(kv->base);
+        kv->base = nullptr;
+        kv->ctx = nullptr;
+    }
+    for (gla_q8w *w : ctx->q8ws) detach_q8w(w);
     if (ctx->dstage) (void)hipFree(ctx->dstage);
     if (ctx->hstage) (void)hipHostFree(ctx->hstage);
     for (const auto &r : ctx->retired) {
@@ -276,6 +282,15 @@ int gla_memcpy_dtoh(gla_ctx *ctx, void *dst_host, const void *src_dev, size_t by
     return GLA_OK;
 }
 
+// A storage or weight handle used with `ctx` must have been created on it (and
+// not be detached by the context's destruction).
+static int check_owner(const gla_ctx *ctx, const gla_kv *kv, const char *fn) {
+    if (kv->ctx != ctx)
+        return set_error(GLA_ERR_INVALID, "%s: the KV storage belongs to %s", fn,
+                         kv->ctx ? "another context" : "a destroyed context");
+    return GLA_OK;
+}
+
 static int kv_alloc(gla_ctx *ctx, gla_kv *kv) {
     const int d = kv->head_dim;
     kv->kv_dim = kv->n_kv_heads * d;
@@ -328,6 +343,7 @@ int gla_kv_cache_create(gla_ctx *ctx, gla_kv_dtype dtype, int n_seqs, int n_laye
         delete kv;
         return rc;
     }
+    ctx->kvs.push_back(kv);
     *out = kv;
     return GLA_OK;
     GLA_GUARD_END
@@ -352,6 +368,7 @@ int gla_pool_create(gla_ctx *ctx, gla_kv_dtype dtype, int n_kv_heads, int head_d
         delete kv;
         return rc;
     }
+    ctx->kvs.push_back(kv);
     *out = kv;
     return GLA_OK;
     GLA_GUARD_END
@@ -360,11 +377,12 @@ int gla_pool_create(gla_ctx *ctx, gla_kv_dtype dtype, int n_kv_heads, int head_d
 int gla_kv_destroy(gla_kv *kv) {
     GLA_GUARD_BEGIN
     if (!kv) return GLA_OK;
-    if (kv->ctx) {
-        (void)hipSetDevice(kv->ctx->device);
-        (void)hipStreamSynchronize(kv->ctx->stream);
+    if (gla_ctx *ctx = kv->ctx) {  // else its context already freed the storage
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        if (kv->base) (void)hipFree(kv->base);
+        ctx->kvs.erase(std::remove(ctx->kvs.begin(), ctx->kvs.end(), kv), ctx->kvs.end());
     }
-    if (kv->base) (void)hipFree(kv->base);
     delete kv;
     return GLA_OK;
     GLA_GUARD_END
@@ -396,6 +414,7 @@ int gla_kv_write_rows(gla_ctx *ctx, gla_kv *kv, const int64_t *rows_dev, const f
                       const float *v_dev, int n_rows) {
     GLA_GUARD_BEGIN
     GLA_REQUIRE(ctx && kv && n_rows >= 0, "gla_kv_write_rows: bad argument");
+    if (int rc = check_owner(ctx, kv, "gla_kv_write_rows")) return rc;
     if (n_rows == 0) return GLA_OK;
     GLA_REQUIRE(rows_dev && k_dev && v_dev, "gla_kv_write_rows: NULL buffer");
     GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
@@ -407,6 +426,7 @@ int gla_kv_write_rows_host(gla_ctx *ctx, gla_kv *kv, const int64_t *rows, const 
                            int n_rows) {
     GLA_GUARD_BEGIN
     GLA_REQUIRE(ctx && kv && n_rows >= 0, "gla_kv_write_rows_host: bad argument");
+    if (int rc = check_owner(ctx, kv, "gla_kv_write_rows_host")) return rc;
     if (n_rows == 0) return GLA_OK;
     GLA_REQUIRE(rows && k && v, "gla_kv_write_rows_host: NULL buffer");
     int rc = check_rows_host(kv, rows, n_rows);
@@ -437,6 +457,7 @@ int gla_kv_export_rows_host(gla_ctx *ctx, const gla_kv *kv, const int64_t *rows,
                             uint8_t *v_out) {
     GLA_GUARD_BEGIN
     GLA_REQUIRE(ctx && kv && n_rows >= 0, "gla_kv_export_rows_host: bad argument");
+    if (int rc = check_owner(ctx, kv, "gla_kv_export_rows_host")) return rc;
     if (n_rows == 0) return GLA_OK;
     GLA_REQUIRE(rows && k_out && v_out, "gla_kv_export_rows_host: NULL buffer");
     int rc = check_rows_host(kv, rows, n_rows);
@@ -468,6 +489,7 @@ int gla_kv_import_rows_host(gla_ctx *ctx, gla_kv *kv, const int64_t *rows, int n
                             const uint8_t *v_in) {
     GLA_GUARD_BEGIN
     GLA_REQUIRE(ctx && kv && n_rows >= 0, "gla_kv_import_rows_host: bad argument");
+    if (int rc = check_owner(ctx, kv, "gla_kv_import_rows_host")) return rc;
     if (n_rows == 0) return GLA_OK;
     GLA_REQUIRE(rows && k_in && v_in, "gla_kv_import_rows_host: NULL buffer");
     int rc = check_rows_host(kv, rows, n_rows);
@@ -497,6 +519,7 @@ int gla_kv_import_rows_host(gla_ctx *ctx, gla_kv *kv, const int64_t *rows, int n
 int gla_pool_copy_page(gla_ctx *ctx, gla_kv *pool, int src_page, int dst_page) {
     GLA_GUARD_BEGIN
     GLA_REQUIRE(ctx && pool && pool->is_pool, "gla_pool_copy_page: needs a pool");
+    if (int rc = check_owner(ctx, pool, "gla_pool_copy_page")) return rc;
     GLA_REQUIRE(src_page >= 0 && src_page < pool->n_pages && dst_page >= 0 && dst_page < pool->n_pages,
                 "gla_pool_copy_page: page out of range");
     if (src_page == dst_page) return GLA_OK;
@@ -508,6 +531,7 @@ int gla_pool_copy_page(gla_ctx *ctx, gla_kv *pool, int src_page, int dst_page) {
 int gla_pool_zero_page(gla_ctx *ctx, gla_kv *pool, int page) {
     GLA_GUARD_BEGIN
     GLA_REQUIRE(ctx && pool && pool->is_pool, "gla_pool_zero_page: needs a pool");
+    if (int rc = check_owner(ctx, pool, "gla_pool_zero_page")) return rc;
     GLA_REQUIRE(page >= 0 && page < pool->n_pages, "gla_pool_zero_page: page out of range");
     GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
     return launch_zero_pages(ctx, pool, page, 1);
@@ -552,6 +576,7 @@ static int decode_launch_of(gla_ctx *ctx, const gla_decode_args *a, const char *
     *nothing = false;
     GLA_REQUIRE(ctx && a && a->kv, "%s: NULL argument", fn);
     const gla_kv *kv = a->kv;
+    if (int rc = check_owner(ctx, kv, fn)) return rc;
     GLA_REQUIRE(a->n_seqs >= 0, "%s: n_seqs < 0", fn);
     if (a->n_seqs == 0) {
         *nothing = true;
@@ -625,6 +650,7 @@ int gla_prefill(gla_ctx *ctx, const gla_prefill_args *a) {
     GLA_GUARD_BEGIN
     GLA_REQUIRE(ctx && a && a->kv, "gla_prefill: NULL argument");
     const gla_kv *kv = a->kv;
+    if (int rc = check_owner(ctx, kv, "gla_prefill")) return rc;
     GLA_REQUIRE(a->n_seqs >= 0, "gla_prefill: n_seqs < 0");
     if (a->n_seqs == 0 || a->max_q_len == 0) return GLA_OK;
     GLA_REQUIRE(a->q && a->out && a->q_start && a->pos_offset, "gla_prefill: NULL buffer");
@@ -733,6 +759,7 @@ int gla_attention_resident(gla_ctx *ctx, const float *q, const gla_kv *cache, in
                            float *out) {
     GLA_GUARD_BEGIN
     GLA_REQUIRE(ctx && q && out && cache, "gla_attention_resident: NULL argument");
+    if (int rc = check_owner(ctx, cache, "gla_attention_resident")) return rc;
     GLA_REQUIRE(!cache->is_pool, "gla_attention_resident: needs a contiguous cache");
     GLA_REQUIRE(seq >= 0 && seq < cache->n_seqs, "gla_attention_resident: seq out of range");
     GLA_REQUIRE(window_start >= 0 && attend_len >= 0 && (int64_t)window_start + attend_len <= cache->max_seq,

@@ -137,6 +137,11 @@ struct gla_ctx {
     // queued, and any HIP graph captured from the stream, still address them
     // (second: pinned host memory).
     std::vector<std::pair<void *, bool>> retired;
+    // KV storages and weights created on this context: gla_destroy frees
+    // their device memory and detaches the handles, so a handle released
+    // after its context frees only itself.
+    std::vector<gla_kv *> kvs;
+    std::vector<gla_q8w *> q8ws;
 };
 
 struct gla_kv {
@@ -164,6 +169,8 @@ KvLayout layout_of(const gla_kv *kv);
 // doubling; a replaced buffer stays allocated until gla_destroy).
 int ensure_scratch(gla_ctx *ctx, size_t bytes, void **out);
 int ensure_dstage(gla_ctx *ctx, size_t bytes);
+// Free a weight handle's device memory and detach it from its context.
+void detach_q8w(gla_q8w *w);
 int ensure_hstage(gla_ctx *ctx, size_t bytes);
 
 // Launchers (return GLA_OK or an error code with the message set).

@@ -44,6 +44,15 @@ struct gla_q8w {
 };
 
 namespace gla {
+
+void detach_q8w(gla_q8w *w) {
+    if (w->quants) (void)hipFree(w->quants);
+    if (w->scales) (void)hipFree(w->scales);
+    w->quants = nullptr;
+    w->scales = nullptr;
+    w->ctx = nullptr;
+}
+
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -638,24 +647,28 @@ int gla_q8w_create(gla_ctx *ctx, const uint8_t *ggml_host, int rows, int cols, g
         delete w;
         return set_error(GLA_ERR_BUFFER, "gla_q8w_create: %s", hipGetErrorString(e));
     }
+    ctx->q8ws.push_back(w);
     *out = w;
     return GLA_OK;
 }
 
 int gla_q8w_destroy(gla_q8w *w) {
     if (!w) return GLA_OK;
-    if (w->ctx) {
-        (void)hipSetDevice(w->ctx->device);
-        (void)hipStreamSynchronize(w->ctx->stream);
+    if (gla_ctx *ctx = w->ctx) {  // else its context already freed the weights
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        ctx->q8ws.erase(std::remove(ctx->q8ws.begin(), ctx->q8ws.end(), w), ctx->q8ws.end());
+        gla::detach_q8w(w);
     }
-    (void)hipFree(w->quants);
-    (void)hipFree(w->scales);
     delete w;
     return GLA_OK;
 }
 
 int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, float *y) {
     if (!ctx || !w || (n_vec > 0 && (!x || !y))) return set_error(GLA_ERR_INVALID, "gla_matvec_q8_0: NULL argument");
+    if (w->ctx != ctx)
+        return set_error(GLA_ERR_INVALID, "gla_matvec_q8_0: the weights belong to %s",
+                         w->ctx ? "another context" : "a destroyed context");
     if (n_vec < 0) return set_error(GLA_ERR_INVALID, "gla_matvec_q8_0: n_vec %d < 0", n_vec);
     if (n_vec == 0) return GLA_OK;
     GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);

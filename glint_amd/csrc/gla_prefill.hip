@@ -551,6 +551,84 @@ constexpr int kBf16Waves = D == 256 ? 4 : 8;
 // maximum before the maximum, and with it O, is rescaled.
 constexpr float kLazyMax = 8.0f;
 
+// S^T accumulators of a tile before S = K.Q^T: -m (the query's reference
+// maximum) without a soft-cap, so the MFMA returns s - m and p = 2^(s - m)
+// needs no subtraction; 0 with a soft-cap (the cap needs the true score) or
+// before the query's first attended key.
+template <int NT, bool CAP>
+__device__ __forceinline__ void bf16_score_init(floatx4 (&sacc)[2][NT], const float (&m)[NT]) {
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const float init = (CAP || m[nt] == -INFINITY) ? 0.0f : -m[nt];
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) sacc[mt][nt] = floatx4{init, init, init, init};
+    }
+}
+
+// Online softmax of one 32-key tile of the bf16 kernels (both share it, so
+// their results are bit-identical): soft-cap and mask, the lazy maximum
+// (the reference moves only when a score passes it by more than 8 log2
+// units, so p stays at most 256, exact range for bf16 and f32, and the
+// rescale of O is rare), p = 2^(s - m) rounded to bf16 for both MFMAs, and
+// the rescale of O and of the row sums when the reference moves.
+template <int NT, int DT, bool CAP>
+__device__ __forceinline__ void bf16_softmax(floatx4 (&sacc)[2][NT], float (&m)[NT], floatx4 (&lacc)[NT],
+                                             floatx4 (&o)[DT][NT], bf16x8 (&pb)[NT], float softcap, bool interior,
+                                             int kbase, const int (&qpos)[NT], const int (&qlo)[NT], int klo,
+                                             int khi) {
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        floatx4 col[2] = {sacc[0][nt], sacc[1][nt]};
+        cap_and_mask<CAP>(col, softcap, interior, kbase, qpos[nt], qlo[nt], klo, khi);
+        float mx = fmaxf(fmaxf(fmaxf(col[0][0], col[0][1]), fmaxf(col[0][2], col[0][3])),
+                         fmaxf(fmaxf(col[1][0], col[1][1]), fmaxf(col[1][2], col[1][3])));
+        mx = max_rows4(mx);
+        float m_new, shift;  // the new reference; what this tile's scores lose
+        if constexpr (CAP) {
+            m_new = (mx > m[nt] + kLazyMax || (m[nt] == -INFINITY && mx != -INFINITY)) ? mx : m[nt];
+            shift = m_new == -INFINITY ? 0.0f : m_new;
+        } else if (m[nt] == -INFINITY) {  // scores are absolute until the first attended key
+            m_new = mx;
+            shift = mx == -INFINITY ? 0.0f : mx;
+        } else {
+            const bool up = mx > kLazyMax;
+            m_new = up ? m[nt] + mx : m[nt];
+            shift = up ? mx : 0.0f;
+        }
+        const float rs = (m[nt] != -INFINITY && m_new != m[nt]) ? fast_exp2(m[nt] - m_new) : 1.0f;
+        m[nt] = m_new;
+        if (CAP || __ballot(shift != 0.0f)) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                col[0][i] -= shift;
+                col[1][i] -= shift;
+            }
+        }
+        float pr[2][4];
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) pr[mt][i] = fast_exp2(col[mt][i]);
+        pb[nt] = bf16x8{(__bf16)pr[0][0], (__bf16)pr[0][1], (__bf16)pr[0][2], (__bf16)pr[0][3],
+                        (__bf16)pr[1][0], (__bf16)pr[1][1], (__bf16)pr[1][2], (__bf16)pr[1][3]};
+        if (__ballot(rs != 1.0f)) {
+#pragma unroll
+            for (int t = 0; t < DT; t++) o[t][nt] *= rs;
+            lacc[nt] *= rs;
+        }
+    }
+}
+
+// Row sums of the tile's bf16 probabilities, from one MFMA against an
+// all-ones operand: every element of a lane accumulates its query's sum.
+template <int NT>
+__device__ __forceinline__ void bf16_row_sums(floatx4 (&lacc)[NT], const bf16x8 (&pb)[NT]) {
+    const bf16x8 ones = bf16x8{(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f,
+                               (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) lacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[nt], lacc[nt], 0, 0, 0);
+}
+
 template <int D, bool Q8, bool CAP>
 __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const PrefillParams p) {
     constexpr int NW = kBf16Waves<D>, NT = 2, NTHR = NW * 64;
@@ -608,20 +686,22 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
     }
 
     floatx4 o[DT][NT];
-#pragma unroll
-    for (int t = 0; t < DT; t++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) o[t][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m[NT], lpart[NT];
+    floatx4 lacc[NT];
+    float m[NT];
     int qpos[NT], qlo[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+        for (int t = 0; t < DT; t++) o[t][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        lacc[nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         m[nt] = -INFINITY;
-        lpart[nt] = 0.0f;
         const int lq = wq0 + nt * 16 + lrow;
         qpos[nt] = lq < q_len ? pos0 + lq : -1;
         qlo[nt] = window_lo(pos0 + lq, p.sliding_window);
     }
+    // keys this wave's queries attend: [wlo, whi]
+    const int whi = min(khi, pos0 + wq0 + QW - 1);
+    const int wlo = max(klo, window_lo(pos0 + wq0, p.sliding_window));
 
     if (khi >= klo) {
         const int kfirst = (klo / KT) * KT;
@@ -635,13 +715,11 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
             if (more) fetch_tile_bf16<D, NTHR, Q8>(p, b, kvh, k0 + KT, klo, khi, tb);
             const __bf16 *kh = Kh[buf];
             const __bf16 *vt = Vt[buf];
-
-            // S^T = K . Q^T
+            // a tile wholly past this wave's last query or before its window adds nothing
+            if (k0 <= whi && k0 + KT - 1 >= wlo) {
+            // S^T = K . Q^T (minus the reference maximum, see bf16_score_init)
             floatx4 sacc[2][NT];
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) sacc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            bf16_score_init<NT, CAP>(sacc, m);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 bf16x8 a[2];
@@ -658,49 +736,10 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
             const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
                                   (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
             bf16x8 pb[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                floatx4 col[2] = {sacc[0][nt], sacc[1][nt]};
-                cap_and_mask<CAP>(col, p.softcap, interior, k0 + 4 * lgrp, qpos[nt], qlo[nt], klo, khi);
-                sacc[0][nt] = col[0];
-                sacc[1][nt] = col[1];
-                float mx = -INFINITY;
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) mx = fmaxf(mx, sacc[mt][nt][i]);
-                mx = max_rows4(mx);
-                // Lazy maximum: the row's reference moves only when a score
-                // passes it by more than 8 (log2 units), so p = 2^(s - m) stays
-                // at most 256 (exact range for bf16 and f32) and the rescale of
-                // O is rare; O / l is unchanged.
-                const bool up = mx > m[nt] + kLazyMax;
-                const float m_new = up ? mx : m[nt];
-                if (m_new == -INFINITY) {
-                    pb[nt] = bf16x8{};
-                    continue;
-                }
-                const float rs = up ? fast_exp2(m[nt] - m_new) : 1.0f;
-                m[nt] = m_new;
-                float pr[2][4];
-                float ls = 0.0f;
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        pr[mt][i] = fast_exp2(sacc[mt][nt][i] - m_new);
-                        ls += pr[mt][i];  // the f32 p; the MFMA takes it rounded to bf16
-                    }
-                pb[nt] = bf16x8{(__bf16)pr[0][0], (__bf16)pr[0][1], (__bf16)pr[0][2], (__bf16)pr[0][3],
-                                (__bf16)pr[1][0], (__bf16)pr[1][1], (__bf16)pr[1][2], (__bf16)pr[1][3]};
-                lpart[nt] = lpart[nt] * rs + ls;
-                if (__ballot(rs != 1.0f)) {
-#pragma unroll
-                    for (int t = 0; t < DT; t++) o[t][nt] *= rs;
-                }
-            }
+            bf16_softmax<NT, DT, CAP>(sacc, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo, khi);
 
-            // O^T += V^T . P^T
+            // O^T += V^T . P^T, and the row sums
+            bf16_row_sums<NT>(lacc, pb);
 #pragma unroll
             for (int t = 0; t < DT; t++) {
                 const __bf16 *vr = vt + (16 * t + lrow) * kVtRowH;
@@ -711,6 +750,7 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
                 for (int nt = 0; nt < NT; nt++)
                     o[t][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[nt], o[t][nt], 0, 0, 0);
             }
+            }
 
             if (more) store_tile_bf16<D, NTHR>(tb, Kh[buf ^ 1], Vt[buf ^ 1]);
             __syncthreads();
@@ -720,8 +760,7 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
     // normalise and store: lane holds O^T[d = 16t + 4*lgrp + r][query lrow]
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        float lt = lpart[nt];
-        lt = sum_rows4(lt);
+        const float lt = lacc[nt][0];
         const int lq = wq0 + nt * 16 + lrow;
         if (lq >= q_len) continue;
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
@@ -822,27 +861,13 @@ __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-// Wait until at most n (wave-uniform, 0..16) vector-memory loads are
-// outstanding; larger n waits for all.
-__device__ __forceinline__ void wait_vm_upto(int n) {
-    switch (n) {
-#define GLA_WAIT_CASE(k) \
-    case k:              \
-        wait_vm<k>();    \
-        break;
-        GLA_WAIT_CASE(1) GLA_WAIT_CASE(2) GLA_WAIT_CASE(3) GLA_WAIT_CASE(4) GLA_WAIT_CASE(5) GLA_WAIT_CASE(6)
-        GLA_WAIT_CASE(7) GLA_WAIT_CASE(8) GLA_WAIT_CASE(9) GLA_WAIT_CASE(10) GLA_WAIT_CASE(11) GLA_WAIT_CASE(12)
-        GLA_WAIT_CASE(13) GLA_WAIT_CASE(14) GLA_WAIT_CASE(15) GLA_WAIT_CASE(16)
-#undef GLA_WAIT_CASE
-    default:
-        wait_vm<0>();
-    }
-}
-
 // Waves per workgroup of the staged kernel (32 queries each): as many as the
 // registers allow (d = 64: 4 per SIMD, d = 128: 3, d = 256: 1).
 template <int D>
 constexpr int kBf16sWaves = D == 64 ? 16 : (D == 128 ? 12 : 4);
+// Kilobyte copies per copying wave of the staged kernel's tile ring.
+template <int D>
+constexpr int kCopiesPerWave = D == 64 ? 1 : (D == 128 ? 2 : 8);
 
 template <int D, bool CAP>
 __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(const PrefillParams p,
@@ -898,20 +923,22 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
     }
 
     floatx4 o[DT][NT];
-#pragma unroll
-    for (int t = 0; t < DT; t++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) o[t][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m[NT], lpart[NT];
+    floatx4 lacc[NT];
+    float m[NT];
     int qpos[NT], qlo[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+        for (int t = 0; t < DT; t++) o[t][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        lacc[nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         m[nt] = -INFINITY;
-        lpart[nt] = 0.0f;
         const int lq = wq0 + nt * 16 + lrow;
         qpos[nt] = lq < q_len ? pos0 + lq : -1;
         qlo[nt] = window_lo(pos0 + lq, p.sliding_window);
     }
+    // keys this wave's queries attend: [wlo, whi]
+    const int whi = min(khi, pos0 + wq0 + QW - 1);
+    const int wlo = max(klo, window_lo(pos0 + wq0, p.sliding_window));
 
     if (khi >= klo) {
         const int tfirst = klo / KT;
@@ -919,35 +946,49 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
         const uint8_t *unit_img = img + ((int64_t)b * p.n_kv_heads + kvh) * n_tiles * kTileImage<D>;
         const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(
             (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)&ring[0][0]);
-        // this wave's share of a tile: kilobytes wave, wave + NW, ... (below NC)
-        const int my_copies = wave < NC ? (NC - wave + NW - 1) / NW : 0;
+        // A tile's NC kilobyte copies go to the first NC / CPW waves, CPW each,
+        // so every wave that copies has the same count in flight and one
+        // wait count (chosen by the tiles left) serves every wave.
+        constexpr int CPW = kCopiesPerWave<D>;
+        static_assert(NC % CPW == 0 && NC / CPW <= NW, "copies cover the tile");
         auto issue = [&](int i) {
-            const uint8_t *src = unit_img + (int64_t)(tfirst + i) * kTileImage<D>;
-            const uint32_t dst = ring_lds + (uint32_t)((i % kRingTiles) * kTileImage<D>);
+            if (wave < NC / CPW) {
+                const uint8_t *src = unit_img + (int64_t)(tfirst + i) * kTileImage<D>;
+                const uint32_t dst = ring_lds + (uint32_t)((i % kRingTiles) * kTileImage<D>);
 #pragma unroll
-            for (int c = wave; c < NC; c += NW)
-                lds_copy16(src, (uint32_t)(c * 1024 + lane * 16), dst + c * 1024);
+                for (int c = 0; c < CPW; c++) {
+                    const int piece = wave * CPW + c;
+                    lds_copy16(src, (uint32_t)(piece * 1024 + lane * 16), dst + piece * 1024);
+                }
+            }
         };
 #pragma unroll
         for (int i = 0; i < kRingTiles - 1; i++)
             if (i < n) issue(i);
+        static_assert(kRingTiles == 4, "the waits below assume two tiles in flight behind the current one");
         for (int i = 0; i < n; i++) {
             // this wave's copies of tile i have landed (later tiles may be in flight) ...
-            wait_vm_upto(min(kRingTiles - 2, n - 1 - i) * my_copies);
+            const int ahead = n - 1 - i;
+            if (ahead >= 2)
+                wait_vm<2 * CPW>();
+            else if (ahead == 1)
+                wait_vm<CPW>();
+            else
+                wait_vm<0>();
             // ... and every wave's have; every wave is also done with tile i - 1,
             // whose buffer the next copy reuses
             __syncthreads();
             if (i + kRingTiles - 1 < n) issue(i + kRingTiles - 1);
             const int k0 = (tfirst + i) * KT;
+            // a tile wholly past this wave's last query (the causal diagonal of
+            // the workgroup's later waves) or before its window adds nothing
+            if (k0 > whi || k0 + KT - 1 < wlo) continue;
             const uint8_t *kimg = ring[i % kRingTiles];
             const uint8_t *vimg = kimg + 64 * D;
 
-            // S^T = K . Q^T
+            // S^T = K . Q^T (minus the reference maximum, see bf16_score_init)
             floatx4 sacc[2][NT];
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) sacc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            bf16_score_init<NT, CAP>(sacc, m);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 bf16x8 a[2];
@@ -964,49 +1005,10 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
             const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
                                   (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
             bf16x8 pb[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                floatx4 col[2] = {sacc[0][nt], sacc[1][nt]};
-                cap_and_mask<CAP>(col, p.softcap, interior, k0 + 4 * lgrp, qpos[nt], qlo[nt], klo, khi);
-                sacc[0][nt] = col[0];
-                sacc[1][nt] = col[1];
-                float mx = -INFINITY;
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                    for (int i2 = 0; i2 < 4; i2++) mx = fmaxf(mx, sacc[mt][nt][i2]);
-                mx = max_rows4(mx);
-                // Lazy maximum: the row's reference moves only when a score
-                // passes it by more than 8 (log2 units), so p = 2^(s - m) stays
-                // at most 256 (exact range for bf16 and f32) and the rescale of
-                // O is rare; O / l is unchanged.
-                const bool up = mx > m[nt] + kLazyMax;
-                const float m_new = up ? mx : m[nt];
-                if (m_new == -INFINITY) {
-                    pb[nt] = bf16x8{};
-                    continue;
-                }
-                const float rs = up ? fast_exp2(m[nt] - m_new) : 1.0f;
-                m[nt] = m_new;
-                float pr[2][4];
-                float ls = 0.0f;
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                    for (int i2 = 0; i2 < 4; i2++) {
-                        pr[mt][i2] = fast_exp2(sacc[mt][nt][i2] - m_new);
-                        ls += pr[mt][i2];  // the f32 p; the MFMA takes it rounded to bf16
-                    }
-                pb[nt] = bf16x8{(__bf16)pr[0][0], (__bf16)pr[0][1], (__bf16)pr[0][2], (__bf16)pr[0][3],
-                                (__bf16)pr[1][0], (__bf16)pr[1][1], (__bf16)pr[1][2], (__bf16)pr[1][3]};
-                lpart[nt] = lpart[nt] * rs + ls;
-                if (__ballot(rs != 1.0f)) {
-#pragma unroll
-                    for (int t = 0; t < DT; t++) o[t][nt] *= rs;
-                }
-            }
+            bf16_softmax<NT, DT, CAP>(sacc, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo, khi);
 
-            // O^T += V^T . P^T
+            // O^T += V^T . P^T, and the row sums
+            bf16_row_sums<NT>(lacc, pb);
 #pragma unroll
             for (int t = 0; t < DT; t++) {
                 const bf16x8 a = *reinterpret_cast<const bf16x8 *>(vimg + ((t * 4 + lgrp) * 16 + lrow) * 16);
@@ -1019,8 +1021,7 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
 
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        float lt = lpart[nt];
-        lt = sum_rows4(lt);
+        const float lt = lacc[nt][0];
         const int lq = wq0 + nt * 16 + lrow;
         if (lq >= q_len) continue;
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;

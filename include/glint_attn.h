@@ -74,6 +74,10 @@ const char *gla_last_error(void);
  * the condition GpuBackend::new reports as GpuAdapterNotFound
  * (src/backend/gpu.rs:44-56); the caller then stays on its CPU path. */
 int gla_create(int device, gla_ctx **out);
+/* Frees the context and the device memory of every cache, pool and weight
+ * set created on it; their handles must still be released
+ * (gla_kv_destroy, gla_q8w_destroy), which then frees only the handle, and
+ * any other use of them fails with GLA_ERR_INVALID. */
 int gla_destroy(gla_ctx *ctx);
 
 /* Run subsequent work on `hip_stream` (a hipStream_t); NULL restores the
