@@ -551,72 +551,104 @@ constexpr int kBf16Waves = D == 256 ? 4 : 8;
 // maximum before the maximum, and with it O, is rescaled.
 constexpr float kLazyMax = 8.0f;
 
-// S^T accumulators of a tile before S = K.Q^T: -m (the query's reference
-// maximum) without a soft-cap, so the MFMA returns s - m and p = 2^(s - m)
-// needs no subtraction; 0 with a soft-cap (the cap needs the true score) or
-// before the query's first attended key.
+// S^T accumulators of a tile before S = K.Q^T: -base, base = the query's
+// reference maximum (0 before its first attended key) without a soft-cap, so
+// the MFMA returns s - base and p = 2^(s - m) needs no subtraction while the
+// reference m stays at base; 0 with a soft-cap (the cap needs the true score).
 template <int NT, bool CAP>
-__device__ __forceinline__ void bf16_score_init(floatx4 (&sacc)[2][NT], const float (&m)[NT]) {
+__device__ __forceinline__ void bf16_score_init(floatx4 (&sacc)[2][NT], float (&base)[NT], const float (&m)[NT]) {
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        const float init = (CAP || m[nt] == -INFINITY) ? 0.0f : -m[nt];
+        base[nt] = (CAP || m[nt] == -INFINITY) ? 0.0f : m[nt];
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) sacc[mt][nt] = floatx4{init, init, init, init};
+        for (int mt = 0; mt < 2; mt++) sacc[mt][nt] = floatx4{-base[nt], -base[nt], -base[nt], -base[nt]};
     }
 }
 
-// Online softmax of one 32-key tile of the bf16 kernels (both share it, so
-// their results are bit-identical): soft-cap and mask, the lazy maximum
+// max of three floats as one v_max3_f32 (fmaxf adds a NaN-quieting max per
+// operand in IEEE mode; the scores hold no NaN that would need it)
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// Online softmax of one 32-key tile of the bf16 kernels (both share it),
+// without branches, so the staged kernel can interleave it with the next
+// tile's S MFMAs: soft-cap and (MASK) the causal/window mask, the lazy maximum
 // (the reference moves only when a score passes it by more than 8 log2
 // units, so p stays at most 256, exact range for bf16 and f32, and the
 // rescale of O is rare), p = 2^(s - m) rounded to bf16 for both MFMAs, and
-// the rescale of O and of the row sums when the reference moves.
-template <int NT, int DT, bool CAP>
-__device__ __forceinline__ void bf16_softmax(floatx4 (&sacc)[2][NT], float (&m)[NT], floatx4 (&lacc)[NT],
-                                             floatx4 (&o)[DT][NT], bf16x8 (&pb)[NT], float softcap, bool interior,
-                                             int kbase, const int (&qpos)[NT], const int (&qlo)[NT], int klo,
-                                             int khi) {
+// the factor rs[nt] that O and the row sums take before this tile is added
+// (bf16_rescale). Without a soft-cap the scores arrive as s - base
+// (bf16_score_init); if the reference moved after the scores were taken,
+// by delta = m - base, that is applied here. (A staged kernel that took tile
+// i + 1's scores beside tile i's softmax, to overlap them within a wave, needed
+// 2 waves per SIMD to stay unspilled and ran ~5% slower than 3 waves without.)
+template <int NT, bool CAP, bool MASK>
+__device__ __forceinline__ void bf16_softmax_p(const floatx4 (&sacc)[2][NT], const float (&base)[NT], float (&m)[NT],
+                                               float (&rs)[NT], bf16x8 (&pb)[NT], float softcap, int kbase,
+                                               const int (&qpos)[NT], const int (&qlo)[NT], int klo, int khi) {
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         floatx4 col[2] = {sacc[0][nt], sacc[1][nt]};
-        cap_and_mask<CAP>(col, softcap, interior, kbase, qpos[nt], qlo[nt], klo, khi);
-        float mx = fmaxf(fmaxf(fmaxf(col[0][0], col[0][1]), fmaxf(col[0][2], col[0][3])),
-                         fmaxf(fmaxf(col[1][0], col[1][1]), fmaxf(col[1][2], col[1][3])));
+        cap_and_mask<CAP>(col, softcap, !MASK, kbase, qpos[nt], qlo[nt], klo, khi);
+        float mx = max3f(max3f(col[0][0], col[0][1], col[0][2]), max3f(col[0][3], col[1][0], col[1][1]),
+                         fmaxf(col[1][2], col[1][3]));
         mx = max_rows4(mx);
+        // (selects: the conditions differ from lane to lane)
+        const bool first = m[nt] == -INFINITY;  // no attended key yet: scores are absolute
         float m_new, shift;  // the new reference; what this tile's scores lose
         if constexpr (CAP) {
-            m_new = (mx > m[nt] + kLazyMax || (m[nt] == -INFINITY && mx != -INFINITY)) ? mx : m[nt];
+            const bool up = first ? mx != -INFINITY : mx > m[nt] + kLazyMax;
+            m_new = up ? mx : m[nt];
             shift = m_new == -INFINITY ? 0.0f : m_new;
-        } else if (m[nt] == -INFINITY) {  // scores are absolute until the first attended key
-            m_new = mx;
-            shift = mx == -INFINITY ? 0.0f : mx;
+            const float r = fast_exp2(m[nt] - mx);
+            rs[nt] = (up && !first) ? r : 1.0f;
         } else {
-            const bool up = mx > kLazyMax;
-            m_new = up ? m[nt] + mx : m[nt];
-            shift = up ? mx : 0.0f;
+            const float delta = first ? 0.0f : m[nt] - base[nt];
+            const bool up = first ? mx != -INFINITY : mx - delta > kLazyMax;
+            m_new = up ? (first ? mx : m[nt] + (mx - delta)) : m[nt];
+            shift = up ? mx : delta;
+            const float r = fast_exp2(delta - mx);
+            rs[nt] = (up && !first) ? r : 1.0f;
         }
-        const float rs = (m[nt] != -INFINITY && m_new != m[nt]) ? fast_exp2(m[nt] - m_new) : 1.0f;
         m[nt] = m_new;
-        if (CAP || __ballot(shift != 0.0f)) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                col[0][i] -= shift;
-                col[1][i] -= shift;
-            }
-        }
         float pr[2][4];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) pr[mt][i] = fast_exp2(col[mt][i]);
+            for (int i = 0; i < 4; i++) pr[mt][i] = fast_exp2(col[mt][i] - shift);
         pb[nt] = bf16x8{(__bf16)pr[0][0], (__bf16)pr[0][1], (__bf16)pr[0][2], (__bf16)pr[0][3],
                         (__bf16)pr[1][0], (__bf16)pr[1][1], (__bf16)pr[1][2], (__bf16)pr[1][3]};
-        if (__ballot(rs != 1.0f)) {
-#pragma unroll
-            for (int t = 0; t < DT; t++) o[t][nt] *= rs;
-            lacc[nt] *= rs;
-        }
     }
+}
+
+// O and the row sums take the factor of a moved reference (rare: a wave-uniform
+// branch per query tile).
+template <int NT, int DT>
+__device__ __forceinline__ void bf16_rescale(const float (&rs)[NT], floatx4 (&lacc)[NT], floatx4 (&o)[DT][NT]) {
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+        if (__ballot(rs[nt] != 1.0f)) {
+#pragma unroll
+            for (int t = 0; t < DT; t++) o[t][nt] *= rs[nt];
+            lacc[nt] *= rs[nt];
+        }
+}
+
+// The whole softmax of a tile whose mask need is known at run time.
+template <int NT, int DT, bool CAP>
+__device__ __forceinline__ void bf16_softmax(floatx4 (&sacc)[2][NT], const float (&base)[NT], float (&m)[NT],
+                                             floatx4 (&lacc)[NT], floatx4 (&o)[DT][NT], bf16x8 (&pb)[NT],
+                                             float softcap, bool interior, int kbase, const int (&qpos)[NT],
+                                             const int (&qlo)[NT], int klo, int khi) {
+    float rs[NT];
+    if (interior)
+        bf16_softmax_p<NT, CAP, false>(sacc, base, m, rs, pb, softcap, kbase, qpos, qlo, klo, khi);
+    else
+        bf16_softmax_p<NT, CAP, true>(sacc, base, m, rs, pb, softcap, kbase, qpos, qlo, klo, khi);
+    bf16_rescale<NT, DT>(rs, lacc, o);
 }
 
 // Row sums of the tile's bf16 probabilities, from one MFMA against an
@@ -687,7 +719,7 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
 
     floatx4 o[DT][NT];
     floatx4 lacc[NT];
-    float m[NT];
+    float m[NT];  // the query's reference maximum (log2 domain)
     int qpos[NT], qlo[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
@@ -719,7 +751,8 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
             if (k0 <= whi && k0 + KT - 1 >= wlo) {
             // S^T = K . Q^T (minus the reference maximum, see bf16_score_init)
             floatx4 sacc[2][NT];
-            bf16_score_init<NT, CAP>(sacc, m);
+            float base[NT];
+            bf16_score_init<NT, CAP>(sacc, base, m);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 bf16x8 a[2];
@@ -736,7 +769,8 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
             const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
                                   (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
             bf16x8 pb[NT];
-            bf16_softmax<NT, DT, CAP>(sacc, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo, khi);
+            bf16_softmax<NT, DT, CAP>(sacc, base, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo,
+                                      khi);
 
             // O^T += V^T . P^T, and the row sums
             bf16_row_sums<NT>(lacc, pb);
@@ -862,7 +896,7 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 // Waves per workgroup of the staged kernel (32 queries each): as many as the
-// registers allow (d = 64: 4 per SIMD, d = 128: 3, d = 256: 1).
+// registers allow without spilling (d = 64: 4 per SIMD, d = 128: 3, d = 256: 1).
 template <int D>
 constexpr int kBf16sWaves = D == 64 ? 16 : (D == 128 ? 12 : 4);
 // Kilobyte copies per copying wave of the staged kernel's tile ring.
@@ -988,7 +1022,8 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
 
             // S^T = K . Q^T (minus the reference maximum, see bf16_score_init)
             floatx4 sacc[2][NT];
-            bf16_score_init<NT, CAP>(sacc, m);
+            float base[NT];
+            bf16_score_init<NT, CAP>(sacc, base, m);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 bf16x8 a[2];
@@ -1005,7 +1040,8 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
             const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
                                   (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
             bf16x8 pb[NT];
-            bf16_softmax<NT, DT, CAP>(sacc, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo, khi);
+            bf16_softmax<NT, DT, CAP>(sacc, base, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo,
+                                      khi);
 
             // O^T += V^T . P^T, and the row sums
             bf16_row_sums<NT>(lacc, pb);
