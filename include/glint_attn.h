@@ -81,7 +81,11 @@ int gla_create(int device, gla_ctx **out);
 int gla_destroy(gla_ctx *ctx);
 
 /* Run subsequent work on `hip_stream` (a hipStream_t); NULL restores the
- * context's own stream. */
+ * context's own stream. Each stream the context has launched work on has
+ * its own device scratch (decode split partials, bf16 prefill tile images,
+ * matvec activation pieces), so calls queued on different streams at once
+ * never share it and may overlap; calls on one stream run in order as usual.
+ * The context itself is not thread-safe: switch streams from one thread. */
 int gla_set_stream(gla_ctx *ctx, void *hip_stream);
 /* The hipStream_t work is enqueued on. */
 void *gla_get_stream(gla_ctx *ctx);
