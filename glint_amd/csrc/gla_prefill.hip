@@ -48,13 +48,22 @@ struct PrefillParams {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max of two floats as one v_max_f32: fmaxf adds a NaN-quieting max per
+// operand in IEEE mode, and the scores hold no signaling NaN that would need
+// it (a quiet NaN operand still yields the other operand, as fmaxf does).
+__device__ __forceinline__ float max2f(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // max / sum over the four 16-lane rows (lane ^ 16, lane ^ 32) with the gfx950
 // row swaps: VALU only, no LDS round trip.
 __device__ __forceinline__ float max_rows4(float x) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    x = max2f(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+    return max2f(__uint_as_float(c[0]), __uint_as_float(c[1]));
 }
 __device__ __forceinline__ float sum_rows4(float x) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -550,23 +559,25 @@ constexpr int kBf16Waves = D == 256 ? 4 : 8;
 // bf16 softmax: how far (log2 units) a score may pass the row's running
 // maximum before the maximum, and with it O, is rescaled.
 constexpr float kLazyMax = 8.0f;
+// The bf16 kernels' reference maximum before a query's first attended key:
+// finite, so the first attended tile is an ordinary move of the reference
+// (its factor 2^(-1e30 - max) = 0 scales the still-zero O and sums) and the
+// per-tile logic needs no "no key yet" case; a masked score (-inf) still
+// gives p = 0, and a query that attends no key keeps l = 0 (output 0).
+constexpr float kMInit = -1e30f;
 
-// S^T accumulators of a tile before S = K.Q^T: -base, base = the query's
-// reference maximum (0 before its first attended key) without a soft-cap, so
-// the MFMA returns s - base and p = 2^(s - m) needs no subtraction while the
-// reference m stays at base; 0 with a soft-cap (the cap needs the true score).
-template <int NT, bool CAP>
-__device__ __forceinline__ void bf16_score_init(floatx4 (&sacc)[2][NT], float (&base)[NT], const float (&m)[NT]) {
+// S^T accumulators of a tile before S = K.Q^T: zero (the first MFMA takes an
+// inline 0), so the scores arrive absolute and p = 2^(s - m) takes one
+// subtraction per score.
+template <int NT>
+__device__ __forceinline__ void bf16_score_init(floatx4 (&sacc)[2][NT]) {
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        base[nt] = (CAP || m[nt] == -INFINITY) ? 0.0f : m[nt];
+    for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) sacc[mt][nt] = floatx4{-base[nt], -base[nt], -base[nt], -base[nt]};
-    }
+        for (int mt = 0; mt < 2; mt++) sacc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 }
 
-// max of three floats as one v_max3_f32 (fmaxf adds a NaN-quieting max per
-// operand in IEEE mode; the scores hold no NaN that would need it)
+// max of three floats as one v_max3_f32 (no NaN-quieting maxes, as max2f)
 __device__ __forceinline__ float max3f(float a, float b, float c) {
     float r;
     asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
@@ -574,51 +585,35 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
 }
 
 // Online softmax of one 32-key tile of the bf16 kernels (both share it),
-// without branches, so the staged kernel can interleave it with the next
-// tile's S MFMAs: soft-cap and (MASK) the causal/window mask, the lazy maximum
-// (the reference moves only when a score passes it by more than 8 log2
-// units, so p stays at most 256, exact range for bf16 and f32, and the
+// without branches: soft-cap and (MASK) the causal/window mask, the lazy
+// maximum (the reference moves only when a score passes it by more than 8
+// log2 units, so p stays at most 256, exact range for bf16 and f32, and the
 // rescale of O is rare), p = 2^(s - m) rounded to bf16 for both MFMAs, and
 // the factor rs[nt] that O and the row sums take before this tile is added
-// (bf16_rescale). Without a soft-cap the scores arrive as s - base
-// (bf16_score_init); if the reference moved after the scores were taken,
-// by delta = m - base, that is applied here. (A staged kernel that took tile
-// i + 1's scores beside tile i's softmax, to overlap them within a wave, needed
-// 2 waves per SIMD to stay unspilled and ran ~5% slower than 3 waves without.)
+// (bf16_rescale). (A staged kernel that took tile i + 1's scores beside tile
+// i's softmax, to overlap them within a wave, needed 2 waves per SIMD to stay
+// unspilled and ran ~5% slower than 3 waves without.)
 template <int NT, bool CAP, bool MASK>
-__device__ __forceinline__ void bf16_softmax_p(const floatx4 (&sacc)[2][NT], const float (&base)[NT], float (&m)[NT],
-                                               float (&rs)[NT], bf16x8 (&pb)[NT], float softcap, int kbase,
-                                               const int (&qpos)[NT], const int (&qlo)[NT], int klo, int khi) {
+__device__ __forceinline__ void bf16_softmax_p(const floatx4 (&sacc)[2][NT], float (&m)[NT], float (&rs)[NT],
+                                               bf16x8 (&pb)[NT], float softcap, int kbase, const int (&qpos)[NT],
+                                               const int (&qlo)[NT], int klo, int khi) {
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         floatx4 col[2] = {sacc[0][nt], sacc[1][nt]};
         cap_and_mask<CAP>(col, softcap, !MASK, kbase, qpos[nt], qlo[nt], klo, khi);
         float mx = max3f(max3f(col[0][0], col[0][1], col[0][2]), max3f(col[0][3], col[1][0], col[1][1]),
-                         fmaxf(col[1][2], col[1][3]));
+                         max2f(col[1][2], col[1][3]));
         mx = max_rows4(mx);
         // (selects: the conditions differ from lane to lane)
-        const bool first = m[nt] == -INFINITY;  // no attended key yet: scores are absolute
-        float m_new, shift;  // the new reference; what this tile's scores lose
-        if constexpr (CAP) {
-            const bool up = first ? mx != -INFINITY : mx > m[nt] + kLazyMax;
-            m_new = up ? mx : m[nt];
-            shift = m_new == -INFINITY ? 0.0f : m_new;
-            const float r = fast_exp2(m[nt] - mx);
-            rs[nt] = (up && !first) ? r : 1.0f;
-        } else {
-            const float delta = first ? 0.0f : m[nt] - base[nt];
-            const bool up = first ? mx != -INFINITY : mx - delta > kLazyMax;
-            m_new = up ? (first ? mx : m[nt] + (mx - delta)) : m[nt];
-            shift = up ? mx : delta;
-            const float r = fast_exp2(delta - mx);
-            rs[nt] = (up && !first) ? r : 1.0f;
-        }
-        m[nt] = m_new;
+        const float m_old = m[nt];
+        const bool up = mx - m_old > kLazyMax;
+        m[nt] = up ? mx : m_old;
+        rs[nt] = up ? fast_exp2(m_old - mx) : 1.0f;
         float pr[2][4];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) pr[mt][i] = fast_exp2(col[mt][i] - shift);
+            for (int i = 0; i < 4; i++) pr[mt][i] = fast_exp2(col[mt][i] - m[nt]);
         pb[nt] = bf16x8{(__bf16)pr[0][0], (__bf16)pr[0][1], (__bf16)pr[0][2], (__bf16)pr[0][3],
                         (__bf16)pr[1][0], (__bf16)pr[1][1], (__bf16)pr[1][2], (__bf16)pr[1][3]};
     }
@@ -639,15 +634,15 @@ __device__ __forceinline__ void bf16_rescale(const float (&rs)[NT], floatx4 (&la
 
 // The whole softmax of a tile whose mask need is known at run time.
 template <int NT, int DT, bool CAP>
-__device__ __forceinline__ void bf16_softmax(floatx4 (&sacc)[2][NT], const float (&base)[NT], float (&m)[NT],
+__device__ __forceinline__ void bf16_softmax(floatx4 (&sacc)[2][NT], float (&m)[NT],
                                              floatx4 (&lacc)[NT], floatx4 (&o)[DT][NT], bf16x8 (&pb)[NT],
                                              float softcap, bool interior, int kbase, const int (&qpos)[NT],
                                              const int (&qlo)[NT], int klo, int khi) {
     float rs[NT];
     if (interior)
-        bf16_softmax_p<NT, CAP, false>(sacc, base, m, rs, pb, softcap, kbase, qpos, qlo, klo, khi);
+        bf16_softmax_p<NT, CAP, false>(sacc, m, rs, pb, softcap, kbase, qpos, qlo, klo, khi);
     else
-        bf16_softmax_p<NT, CAP, true>(sacc, base, m, rs, pb, softcap, kbase, qpos, qlo, klo, khi);
+        bf16_softmax_p<NT, CAP, true>(sacc, m, rs, pb, softcap, kbase, qpos, qlo, klo, khi);
     bf16_rescale<NT, DT>(rs, lacc, o);
 }
 
@@ -726,7 +721,7 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
 #pragma unroll
         for (int t = 0; t < DT; t++) o[t][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         lacc[nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        m[nt] = -INFINITY;
+        m[nt] = kMInit;
         const int lq = wq0 + nt * 16 + lrow;
         qpos[nt] = lq < q_len ? pos0 + lq : -1;
         qlo[nt] = window_lo(pos0 + lq, p.sliding_window);
@@ -749,10 +744,9 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
             const __bf16 *vt = Vt[buf];
             // a tile wholly past this wave's last query or before its window adds nothing
             if (k0 <= whi && k0 + KT - 1 >= wlo) {
-            // S^T = K . Q^T (minus the reference maximum, see bf16_score_init)
+            // S^T = K . Q^T
             floatx4 sacc[2][NT];
-            float base[NT];
-            bf16_score_init<NT, CAP>(sacc, base, m);
+            bf16_score_init<NT>(sacc);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 bf16x8 a[2];
@@ -769,7 +763,7 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
             const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
                                   (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
             bf16x8 pb[NT];
-            bf16_softmax<NT, DT, CAP>(sacc, base, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo,
+            bf16_softmax<NT, DT, CAP>(sacc, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo,
                                       khi);
 
             // O^T += V^T . P^T, and the row sums
@@ -965,7 +959,7 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
 #pragma unroll
         for (int t = 0; t < DT; t++) o[t][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         lacc[nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        m[nt] = -INFINITY;
+        m[nt] = kMInit;
         const int lq = wq0 + nt * 16 + lrow;
         qpos[nt] = lq < q_len ? pos0 + lq : -1;
         qlo[nt] = window_lo(pos0 + lq, p.sliding_window);
@@ -1020,10 +1014,9 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
             const uint8_t *kimg = ring[i % kRingTiles];
             const uint8_t *vimg = kimg + 64 * D;
 
-            // S^T = K . Q^T (minus the reference maximum, see bf16_score_init)
+            // S^T = K . Q^T
             floatx4 sacc[2][NT];
-            float base[NT];
-            bf16_score_init<NT, CAP>(sacc, base, m);
+            bf16_score_init<NT>(sacc);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 bf16x8 a[2];
@@ -1040,7 +1033,7 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
             const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
                                   (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
             bf16x8 pb[NT];
-            bf16_softmax<NT, DT, CAP>(sacc, base, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo,
+            bf16_softmax<NT, DT, CAP>(sacc, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo,
                                       khi);
 
             // O^T += V^T . P^T, and the row sums
