@@ -805,7 +805,8 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
 // Staged bf16 path: a pre-pass converts each (sequence, KV head, 32-key tile)
 // the prefill reads to bf16 once, in the exact LDS image the MFMA operand
 // reads want, and the main kernel copies tile images into an LDS ring with
-// direct global->LDS loads (no registers, no conversion, three tiles ahead).
+// direct global->LDS loads (no registers, no conversion, kRingTiles - 1 tiles
+// ahead).
 // The image of a tile is 128*D bytes, 16-byte pieces:
 //   K: piece ((mt*(D/8) + c)*16 + r) = K[key mt*16 + r][dims 8c .. 8c+7]
 //   V: piece ((t*4 + g)*16 + r)      = V[keys 4g..4g+3, 16+4g..16+4g+3][dim 16t + r]
@@ -813,7 +814,11 @@ __global__ __launch_bounds__(kBf16Waves<D> * 64) void prefill_bf16_kernel(const 
 // of one 256-byte line: no LDS bank conflicts, and the whole image is one
 // contiguous copy. Keys outside the sequence's window union [window_lo(pos0),
 // last query] are zero, as the in-kernel staging zeroes them.
-constexpr int kRingTiles = 4;
+// Tile images in a workgroup's ring: three (48 KB at d = 128) lets three
+// workgroups share a CU, so one's prologue, epilogue and barrier waits meet
+// the others' matrix work; d = 256 keeps four (one workgroup per CU).
+template <int D>
+constexpr int kRingTiles = D == 256 ? 4 : 3;
 
 template <int D>
 constexpr int kTileImage = 128 * D;
@@ -889,23 +894,28 @@ __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-// Waves per workgroup of the staged kernel (32 queries each): as many as the
-// registers allow without spilling (d = 64: 4 per SIMD, d = 128: 3, d = 256: 1).
+// Waves per workgroup of the staged kernel (32 queries each): one per SIMD;
+// a CU holds several workgroups.
 template <int D>
-constexpr int kBf16sWaves = D == 64 ? 16 : (D == 128 ? 12 : 4);
-// Kilobyte copies per copying wave of the staged kernel's tile ring.
+constexpr int kBf16sWaves = 4;
+// Kilobyte copies per wave of the staged kernel's tile ring (every wave copies).
 template <int D>
-constexpr int kCopiesPerWave = D == 64 ? 1 : (D == 128 ? 2 : 8);
+constexpr int kCopiesPerWave = D == 64 ? 2 : (D == 128 ? 4 : 8);
+// Waves per SIMD the staged kernel's registers are sized for (no spills):
+// d = 64: 4 (<= 128 VGPRs), d = 128: 3 (<= 168), d = 256: 1.
+template <int D>
+constexpr int kBf16sOccupancy = D == 64 ? 4 : (D == 128 ? 3 : 1);
 
 template <int D, bool CAP>
-__global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(const PrefillParams p,
+__global__ __launch_bounds__(kBf16sWaves<D> * 64, kBf16sOccupancy<D>) void prefill_bf16s_kernel(const PrefillParams p,
                                                                           const uint8_t *img, int n_tiles) {
     constexpr int NW = kBf16sWaves<D>, NT = 2;
     constexpr int QW = 16 * NT;
     constexpr int KS = D / 32;
     constexpr int DT = D / 16;
     constexpr int NC = kTileImage<D> / 1024;  // 1 KB copies per tile, dealt to the waves in turn
-    __shared__ __attribute__((aligned(16))) uint8_t ring[kRingTiles][kTileImage<D>];
+    constexpr int RT = kRingTiles<D>;
+    __shared__ __attribute__((aligned(16))) uint8_t ring[RT][kTileImage<D>];
 
     const int n_hgrp = p.group / p.hpw;
     const int unit = blockIdx.x;
@@ -982,7 +992,7 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
         auto issue = [&](int i) {
             if (wave < NC / CPW) {
                 const uint8_t *src = unit_img + (int64_t)(tfirst + i) * kTileImage<D>;
-                const uint32_t dst = ring_lds + (uint32_t)((i % kRingTiles) * kTileImage<D>);
+                const uint32_t dst = ring_lds + (uint32_t)((i % RT) * kTileImage<D>);
 #pragma unroll
                 for (int c = 0; c < CPW; c++) {
                     const int piece = wave * CPW + c;
@@ -991,27 +1001,27 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64) void prefill_bf16s_kernel(cons
             }
         };
 #pragma unroll
-        for (int i = 0; i < kRingTiles - 1; i++)
+        for (int i = 0; i < RT - 1; i++)
             if (i < n) issue(i);
-        static_assert(kRingTiles == 4, "the waits below assume two tiles in flight behind the current one");
+        static_assert(RT == 3 || RT == 4, "the waits below assume one or two tiles in flight behind the current one");
         for (int i = 0; i < n; i++) {
             // this wave's copies of tile i have landed (later tiles may be in flight) ...
             const int ahead = n - 1 - i;
-            if (ahead >= 2)
-                wait_vm<2 * CPW>();
-            else if (ahead == 1)
+            if (RT == 4 && ahead >= 2)
+                wait_vm<(RT - 2) * CPW>();
+            else if (ahead >= 1)
                 wait_vm<CPW>();
             else
                 wait_vm<0>();
             // ... and every wave's have; every wave is also done with tile i - 1,
             // whose buffer the next copy reuses
             __syncthreads();
-            if (i + kRingTiles - 1 < n) issue(i + kRingTiles - 1);
+            if (i + RT - 1 < n) issue(i + RT - 1);
             const int k0 = (tfirst + i) * KT;
             // a tile wholly past this wave's last query (the causal diagonal of
             // the workgroup's later waves) or before its window adds nothing
             if (k0 > whi || k0 + KT - 1 < wlo) continue;
-            const uint8_t *kimg = ring[i % kRingTiles];
+            const uint8_t *kimg = ring[i % RT];
             const uint8_t *vimg = kimg + 64 * D;
 
             // S^T = K . Q^T
