@@ -584,15 +584,17 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
     return r;
 }
 
-// Online softmax of one 32-key tile of the bf16 kernels (both share it),
-// without branches: soft-cap and (MASK) the causal/window mask, the lazy
-// maximum (the reference moves only when a score passes it by more than 8
-// log2 units, so p stays at most 256, exact range for bf16 and f32, and the
-// rescale of O is rare), p = 2^(s - m) rounded to bf16 for both MFMAs, and
-// the factor rs[nt] that O and the row sums take before this tile is added
-// (bf16_rescale). (A staged kernel that took tile i + 1's scores beside tile
-// i's softmax, to overlap them within a wave, needed 2 waves per SIMD to stay
-// unspilled and ran ~5% slower than 3 waves without.)
+// Online softmax of one 32-key tile of the bf16 kernels (both share it):
+// soft-cap and (MASK) the causal/window mask, the lazy maximum (the reference
+// moves only when a score passes it by more than 8 log2 units, so p stays at
+// most 256, exact range for bf16 and f32, and the rescale of O is rare), p =
+// 2^(s - m) rounded to bf16 for both MFMAs, and the factor rs[nt] that O and
+// the row sums take before this tile is added (bf16_rescale). Each lane first
+// takes the maximum of its own 8 scores of a query; only when one of them
+// passes its reference by more than the margin (in some lane of the wave: a
+// wave-uniform branch) does the tile take the row maxima across the query's
+// 4 lanes. A row whose maximum passes has that maximum in one of its lanes,
+// so the rare path makes the decisions that taking every row maximum would.
 template <int NT, bool CAP, bool MASK>
 __device__ __forceinline__ void bf16_softmax_p(const floatx4 (&sacc)[2][NT], float (&m)[NT], float (&rs)[NT],
                                                bf16x8 (&pb)[NT], float softcap, int kbase, const int (&qpos)[NT],
@@ -603,12 +605,15 @@ __device__ __forceinline__ void bf16_softmax_p(const floatx4 (&sacc)[2][NT], flo
         cap_and_mask<CAP>(col, softcap, !MASK, kbase, qpos[nt], qlo[nt], klo, khi);
         float mx = max3f(max3f(col[0][0], col[0][1], col[0][2]), max3f(col[0][3], col[1][0], col[1][1]),
                          max2f(col[1][2], col[1][3]));
-        mx = max_rows4(mx);
-        // (selects: the conditions differ from lane to lane)
         const float m_old = m[nt];
-        const bool up = mx - m_old > kLazyMax;
-        m[nt] = up ? mx : m_old;
-        rs[nt] = up ? fast_exp2(m_old - mx) : 1.0f;
+        rs[nt] = 1.0f;
+        if (__ballot(mx - m_old > kLazyMax)) {
+            mx = max_rows4(mx);
+            // (selects: the conditions differ from lane to lane)
+            const bool up = mx - m_old > kLazyMax;
+            m[nt] = up ? mx : m_old;
+            rs[nt] = up ? fast_exp2(m_old - mx) : 1.0f;
+        }
         float pr[2][4];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
@@ -1058,17 +1063,33 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64, kBf16sOccupancy<D>) void prefi
         }
     }
 
+    // Output rows through LDS (the ring is free once every wave is done with
+    // it): a lane holds 4 dims of one query, so direct stores would write
+    // half lines; read back row-major, each store instruction writes whole
+    // D-float rows. Each wave stages its 16 queries of one nt at a time in
+    // its own region (rows padded by 4 floats against bank conflicts); a
+    // wave's LDS operations run in order, so it needs no barrier of its own.
+    constexpr int SROW = D + 4;
+    static_assert(NW * 16 * SROW * 4 <= kRingTiles<D> * kTileImage<D>, "output staging fits the ring");
+    __syncthreads();
+    float *stage = reinterpret_cast<float *>(&ring[0][0]) + wave * 16 * SROW;
+    constexpr int LPR = D / 4;    // lanes per row (16 bytes each)
+    constexpr int RPI = 64 / LPR;  // rows per store instruction
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const float lt = lacc[nt][0];
-        const int lq = wq0 + nt * 16 + lrow;
-        if (lq >= q_len) continue;
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-        float *op = p.out + ((int64_t)(row0 + lq) * p.n_heads + head) * D;
 #pragma unroll
-        for (int t = 0; t < DT; t++) {
-            const floatx4 v = o[t][nt] * inv;
-            *reinterpret_cast<float4 *>(op + 16 * t + 4 * lgrp) = make_float4(v[0], v[1], v[2], v[3]);
+        for (int t = 0; t < DT; t++)
+            *reinterpret_cast<floatx4 *>(stage + lrow * SROW + 16 * t + 4 * lgrp) = o[t][nt] * inv;
+#pragma unroll
+        for (int k = 0; k < 16 / RPI; k++) {
+            const int r = k * RPI + lane / LPR;
+            const int c = (lane % LPR) * 4;
+            const floatx4 v = *reinterpret_cast<const floatx4 *>(stage + r * SROW + c);
+            const int lq = wq0 + nt * 16 + r;
+            if (lq < q_len)
+                *reinterpret_cast<floatx4 *>(p.out + ((int64_t)(row0 + lq) * p.n_heads + head) * D + c) = v;
         }
     }
 }
