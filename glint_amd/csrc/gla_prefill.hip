@@ -842,6 +842,79 @@ __global__ __launch_bounds__(256) void stage_bf16_kernel(const PrefillParams p, 
     const int k0 = t * KT;
     if (khi < klo || k0 > khi || k0 + KT - 1 < klo) return;  // a tile no query of the sequence reads
 
+    uint8_t *dst = img + (((int64_t)b * p.n_kv_heads + kvh) * n_tiles + t) * kTileImage<D>;
+    constexpr int NP = 4 * D;  // pieces of K (and of V) per tile
+    if constexpr (!Q8) {
+        // f32 cache: a K piece is 8 consecutive dims of one key, read and
+        // converted straight from the row; V pieces run across keys, so V
+        // goes through LDS as bf16 rows. The tile's 32 keys lie in two pages.
+        __shared__ __attribute__((aligned(16))) __bf16 Vh[KT][D + 8];
+        const int64_t head_off = (int64_t)kvh * p.kv.head_stride;
+        const int64_t pid0 = map_page(p.pm, b, min(k0, khi) >> 4);
+        const int64_t pid1 = map_page(p.pm, b, min(k0 + 16, khi) >> 4);
+        // every load of the thread is issued before any store (the stores to
+        // the image could alias the cache for the compiler)
+        constexpr int NV = KT * (D / 8) / 256;  // V (key, 8 dims) runs per thread
+        constexpr int NK = NP / 256;            // K pieces per thread
+        float4 va[NV][2], ka[NK][2];
+#pragma unroll
+        for (int r = 0; r < NV; r++) {
+            const int u = threadIdx.x + 256 * r;
+            const int key = u / (D / 8);
+            const int kp = k0 + key;
+            va[r][0] = va[r][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (kp >= klo && kp <= khi) {
+                const float *vr = reinterpret_cast<const float *>(
+                    p.kv.v + (key < 16 ? pid0 : pid1) * p.kv.page_stride + head_off +
+                    (int64_t)(kp & 15) * p.kv.row_stride) + 8 * (u - key * (D / 8));
+                va[r][0] = *reinterpret_cast<const float4 *>(vr);
+                va[r][1] = *reinterpret_cast<const float4 *>(vr + 4);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NK; r++) {
+            const int i = threadIdx.x + 256 * r;
+            const int mt = i / (D / 8 * 16);
+            const int rem = i - mt * (D / 8 * 16);
+            const int key = mt * 16 + (rem & 15);
+            const int kp = k0 + key;
+            ka[r][0] = ka[r][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (kp >= klo && kp <= khi) {
+                const float *kr = reinterpret_cast<const float *>(
+                    p.kv.k + (key < 16 ? pid0 : pid1) * p.kv.page_stride + head_off +
+                    (int64_t)(kp & 15) * p.kv.row_stride) + 8 * (rem >> 4);
+                ka[r][0] = *reinterpret_cast<const float4 *>(kr);
+                ka[r][1] = *reinterpret_cast<const float4 *>(kr + 4);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NV; r++) {
+            const int u = threadIdx.x + 256 * r;
+            const int key = u / (D / 8);
+            const float4 x = va[r][0], y = va[r][1];
+            *reinterpret_cast<bf16x8 *>(&Vh[key][8 * (u - key * (D / 8))]) =
+                bf16x8{(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w,
+                       (__bf16)y.x, (__bf16)y.y, (__bf16)y.z, (__bf16)y.w};
+        }
+        // K pieces, straight to the image
+#pragma unroll
+        for (int r = 0; r < NK; r++) {
+            const float4 x = ka[r][0], y = ka[r][1];
+            *reinterpret_cast<bf16x8 *>(dst + (int64_t)(threadIdx.x + 256 * r) * 16) =
+                bf16x8{(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w,
+                       (__bf16)y.x, (__bf16)y.y, (__bf16)y.z, (__bf16)y.w};
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < NP; i += 256) {
+            const int tt = i >> 6;
+            const int g = (i >> 4) & 3;
+            const int d = 16 * tt + (i & 15);
+            const bf16x8 h = bf16x8{Vh[4 * g][d], Vh[4 * g + 1][d], Vh[4 * g + 2][d], Vh[4 * g + 3][d],
+                                    Vh[16 + 4 * g][d], Vh[17 + 4 * g][d], Vh[18 + 4 * g][d], Vh[19 + 4 * g][d]};
+            *reinterpret_cast<bf16x8 *>(dst + 64 * D + (int64_t)i * 16) = h;
+        }
+        return;
+    }
     __shared__ __attribute__((aligned(16))) float Kf[KT][D + 4];
     __shared__ __attribute__((aligned(16))) float Vf[KT][D + 4];
     for (int u = threadIdx.x; u < (KT / 4) * (D / 4); u += 256) {
@@ -856,8 +929,6 @@ __global__ __launch_bounds__(256) void stage_bf16_kernel(const PrefillParams p, 
         }
     }
     __syncthreads();
-    uint8_t *dst = img + (((int64_t)b * p.n_kv_heads + kvh) * n_tiles + t) * kTileImage<D>;
-    constexpr int NP = 4 * D;  // pieces of K (and of V) per tile
     for (int i = threadIdx.x; i < NP; i += 256) {
         const int mt = i / (D / 8 * 16);
         const int rem = i - mt * (D / 8 * 16);
