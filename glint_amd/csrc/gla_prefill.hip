@@ -977,8 +977,9 @@ constexpr int kBf16sWaves = 4;
 // Kilobyte copies per wave of the staged kernel's tile ring (every wave copies).
 template <int D>
 constexpr int kCopiesPerWave = D == 64 ? 2 : (D == 128 ? 4 : 8);
-// Waves per SIMD the staged kernel's registers are sized for (no spills):
-// d = 64: 4 (<= 128 VGPRs), d = 128: 3 (<= 168), d = 256: 1.
+// Waves per SIMD the staged kernel's registers are sized for: d = 64: 4
+// (<= 128 VGPRs), d = 128: 3 (<= 168; the soft-capped variant spills one
+// register), d = 256: 1.
 template <int D>
 constexpr int kBf16sOccupancy = D == 64 ? 4 : (D == 128 ? 3 : 1);
 

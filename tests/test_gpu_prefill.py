@@ -64,7 +64,7 @@ def test_prefill_paged(backend, dtype, precision):
             assert_close(got[rows], want, *tol, what=f"paged {dtype} {precision} seq {b} window {window}")
 
 
-@pytest.mark.parametrize("d,H,Hkv", [(128, 8, 2), (64, 9, 3), (256, 4, 2)])
+@pytest.mark.parametrize("d,H,Hkv", [(128, 8, 2), (64, 9, 3), (256, 4, 2), (64, 16, 2)])
 @pytest.mark.parametrize("dtype", ["f32", "q8"])
 def test_prefill_bf16_staged_equals_unstaged(backend, monkeypatch, dtype, d, H, Hkv):
     """The bf16 path with the tile images staged once per call (the default) and with each
@@ -84,7 +84,7 @@ def test_prefill_bf16_staged_equals_unstaged(backend, monkeypatch, dtype, d, H, 
         assert np.array_equal(staged.view(np.uint32), unstaged.view(np.uint32)), (dtype, d, cap, window)
 
 
-@pytest.mark.parametrize("d,H,Hkv", [(128, 8, 2), (64, 9, 3), (256, 4, 2), (128, 4, 4)])
+@pytest.mark.parametrize("d,H,Hkv", [(128, 8, 2), (64, 9, 3), (256, 4, 2), (128, 4, 4), (64, 16, 2)])
 @pytest.mark.parametrize("dtype", ["f32", "q8"])
 def test_prefill_bf16_varlen_batch(backend, dtype, d, H, Hkv):
     """bf16-input variant over the varlen batch (chunked offsets, soft-cap, windows): within the
