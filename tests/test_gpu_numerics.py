@@ -244,3 +244,56 @@ def test_prefill_outliers(backend, precision):
             bound = np.maximum(BF16_ABS_TOL, BF16_REL_TOL * mass)
             assert (err <= bound).all(), (b, h, float((err / bound).max()))
             assert_close(want[:, h], f64, 1e-3, 1e-3, what=f"oracle over bf16 inputs vs f64, seq {b} head {h}")
+
+
+# ---------------------------------------------------------------- a running maximum that keeps moving
+@pytest.mark.parametrize("precision", ["f32", "bf16"])
+@pytest.mark.parametrize("window", [None, 64])
+def test_prefill_rising_scores(backend, precision, window):
+    """Scores that climb along the keys (K = noise + (pos / 8) * u, q ~ u): every query's
+    running maximum passes the kernels' lazy threshold (8 log2 units) again and again, so the
+    rescale of O and of the row sums runs on most tiles of every query block, not only on a
+    query's first attended tile as with N(0,1) data."""
+    H, Hkv, d, T = 8, 2, 128, 320
+    kv_dim = Hkv * d
+    rng = np.random.default_rng(7700)
+    u = np.full(d, 4.0 / np.sqrt(d), np.float32)
+    pos = np.arange(T, dtype=np.float32)[:, None]
+    k = 0.5 * rng.standard_normal((T, kv_dim)).astype(np.float32) + (pos / 8.0) * np.tile(u, Hkv)[None, :]
+    v = rng.standard_normal((T, kv_dim)).astype(np.float32)
+    c = Contig(backend, "f32", 1, 1, T, Hkv, d, k=k.reshape(1, 1, T, kv_dim), v=v.reshape(1, 1, T, kv_dim))
+    q = (u[None, None, :] + 0.1 * rng.standard_normal((T, H, d))).astype(np.float32)
+    s = float(1 / np.sqrt(d))
+    # the scores really climb: the last key's score is tens of log2 units above the first's
+    kf = k[:, :d].astype(np.float64)
+    sc = (kf @ q[0, 0].astype(np.float64)) * s / np.log(2.0)
+    assert sc[-1] - sc[0] > 60.0
+    tol = (BF16_ABS_TOL, BF16_REL_TOL) if precision == "bf16" else ()
+    got = run_prefill(backend, c.cache, q, [0, T], [0], H, s, None, window, precision=precision)
+    want = _prefill_oracle(c, 0, q, 0, H, Hkv, d, s, None, window, precision)
+    assert_close(got, want, *tol, what=f"rising scores {precision} window {window}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+@pytest.mark.parametrize("d,H,Hkv", [(64, 9, 3), (128, 32, 8), (256, 16, 8)])
+def test_decode_rising_scores(backend, dtype, d, H, Hkv):
+    """Decode over keys whose scores climb with the position (K = noise + (pos / 8) * u, q ~ u):
+    the running maximum moves on nearly every step of every chunk, and the chunks of a long
+    sequence merge partials whose maxima differ by hundreds of log2 units."""
+    lens = np.array([40, 700, 2100], np.int32)
+    T = int(lens.max())
+    kv_dim = Hkv * d
+    rng = np.random.default_rng(7800 + d)
+    u = np.full(d, 4.0 / np.sqrt(d), np.float32)
+    pos = np.arange(T, dtype=np.float32)[:, None]
+    k = np.stack([0.5 * rng.standard_normal((T, kv_dim)).astype(np.float32) + (pos / 8.0) * np.tile(u, Hkv)[None, :]
+                  for _ in lens])
+    v = rng.standard_normal((len(lens), T, kv_dim)).astype(np.float32)
+    c = Contig(backend, dtype, len(lens), 1, T, Hkv, d, k=k[:, None], v=v[:, None])
+    q = (u[None, None, :] + 0.1 * rng.standard_normal((len(lens), H, d))).astype(np.float32)
+    s = float(1 / np.sqrt(d))
+    for st in (np.zeros(len(lens), np.int32), np.maximum(lens - 300, 0).astype(np.int32)):
+        ln = (lens - st).astype(np.int32)
+        want = _decode_oracle(c, q, st, ln, H, Hkv, d, s, None)
+        got = run_decode(backend, c.cache, q, st, ln, H, s)
+        assert_close(got, want, what=f"{dtype} d{d} rising scores start {st.tolist()}")
