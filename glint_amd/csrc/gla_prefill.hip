@@ -48,14 +48,12 @@ struct PrefillParams {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// max of two floats as one v_max_f32: fmaxf adds a NaN-quieting max per
-// operand in IEEE mode, and the scores hold no signaling NaN that would need
-// it (a quiet NaN operand still yields the other operand, as fmaxf does).
-__device__ __forceinline__ float max2f(float a, float b) {
-    float r;
-    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
+// max of two floats as IEEE-754 maximum (a NaN operand gives NaN): gfx950
+// has v_maximum3_f32, which needs no NaN-quieting max per operand the way
+// fmaxf does after a row swap or a select. Not inline asm: the compiler
+// inserts the wait states an MFMA result needs before a VALU read only for
+// instructions it emits itself, and these maxima read MFMA results directly.
+__device__ __forceinline__ float max2f(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 // max / sum over the four 16-lane rows (lane ^ 16, lane ^ 32) with the gfx950
 // row swaps: VALU only, no LDS round trip.
@@ -577,12 +575,8 @@ __device__ __forceinline__ void bf16_score_init(floatx4 (&sacc)[2][NT]) {
         for (int mt = 0; mt < 2; mt++) sacc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 }
 
-// max of three floats as one v_max3_f32 (no NaN-quieting maxes, as max2f)
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
+// max of three floats as one v_maximum3_f32 (as max2f)
+__device__ __forceinline__ float max3f(float a, float b, float c) { return max2f(max2f(a, b), c); }
 
 // Online softmax of one 32-key tile of the bf16 kernels (both share it):
 // soft-cap and (MASK) the causal/window mask, the lazy maximum (the reference
