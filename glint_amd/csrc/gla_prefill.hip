@@ -631,6 +631,58 @@ __device__ __forceinline__ void bf16_rescale(const float (&rs)[NT], floatx4 (&la
         }
 }
 
+// The softmax of a tile inside every query's causal and window bounds, both
+// query tiles decided by one wave-uniform branch: the row maxima are taken,
+// and references moved, only when some lane's own maximum passes its
+// reference by more than the margin; for a query tile none of whose lanes
+// passes, the rare path moves nothing and scales nothing, so the decisions
+// are bf16_softmax_p's.
+template <int NT, int DT, bool CAP>
+__device__ __forceinline__ void bf16_softmax_interior(floatx4 (&sacc)[2][NT], float (&m)[NT],
+                                                      floatx4 (&lacc)[NT], floatx4 (&o)[DT][NT],
+                                                      bf16x8 (&pb)[NT], float softcap) {
+    float mx[NT];
+    bool pass = false;
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        if constexpr (CAP) {
+            floatx4 col[2] = {sacc[0][nt], sacc[1][nt]};
+            cap_and_mask<CAP>(col, softcap, true, 0, 0, 0, 0, 0);
+            sacc[0][nt] = col[0];
+            sacc[1][nt] = col[1];
+        }
+        mx[nt] = max3f(max3f(sacc[0][nt][0], sacc[0][nt][1], sacc[0][nt][2]),
+                       max3f(sacc[0][nt][3], sacc[1][nt][0], sacc[1][nt][1]), max2f(sacc[1][nt][2], sacc[1][nt][3]));
+        pass = pass || mx[nt] - m[nt] > kLazyMax;
+    }
+    if (__ballot(pass)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const float mr = max_rows4(mx[nt]);
+            // (selects: the conditions differ from lane to lane)
+            const float m_old = m[nt];
+            const bool up = mr - m_old > kLazyMax;
+            m[nt] = up ? mr : m_old;
+            const float rs = up ? fast_exp2(m_old - mr) : 1.0f;
+            if (__ballot(rs != 1.0f)) {
+#pragma unroll
+                for (int t = 0; t < DT; t++) o[t][nt] *= rs;
+                lacc[nt] *= rs;
+            }
+        }
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        float pr[2][4];
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) pr[mt][i] = fast_exp2(sacc[mt][nt][i] - m[nt]);
+        pb[nt] = bf16x8{(__bf16)pr[0][0], (__bf16)pr[0][1], (__bf16)pr[0][2], (__bf16)pr[0][3],
+                        (__bf16)pr[1][0], (__bf16)pr[1][1], (__bf16)pr[1][2], (__bf16)pr[1][3]};
+    }
+}
+
 // The whole softmax of a tile whose mask need is known at run time.
 template <int NT, int DT, bool CAP>
 __device__ __forceinline__ void bf16_softmax(floatx4 (&sacc)[2][NT], float (&m)[NT],
@@ -1075,8 +1127,10 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64, kBf16sOccupancy<D>) void prefi
         for (int i = 0; i < RT - 1; i++)
             if (i < n) issue(i);
         static_assert(RT == 3 || RT == 4, "the waits below assume one or two tiles in flight behind the current one");
-        for (int i = 0; i < n; i++) {
-            // this wave's copies of tile i have landed (later tiles may be in flight) ...
+        // this wave's copies of tile i have landed (later tiles may be in
+        // flight), and every wave's have; every wave is also done with tile
+        // i - 1, whose buffer the next copy reuses
+        auto arrive = [&](int i) {
             const int ahead = n - 1 - i;
             if (RT == 4 && ahead >= 2)
                 wait_vm<(RT - 2) * CPW>();
@@ -1084,19 +1138,11 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64, kBf16sOccupancy<D>) void prefi
                 wait_vm<CPW>();
             else
                 wait_vm<0>();
-            // ... and every wave's have; every wave is also done with tile i - 1,
-            // whose buffer the next copy reuses
             __syncthreads();
             if (i + RT - 1 < n) issue(i + RT - 1);
-            const int k0 = (tfirst + i) * KT;
-            // a tile wholly past this wave's last query (the causal diagonal of
-            // the workgroup's later waves) or before its window adds nothing
-            if (k0 > whi || k0 + KT - 1 < wlo) continue;
-            const uint8_t *kimg = ring[i % RT];
-            const uint8_t *vimg = kimg + 64 * D;
-
-            // S^T = K . Q^T
-            floatx4 sacc[2][NT];
+        };
+        // S^T = K . Q^T of tile i
+        auto scores = [&](const uint8_t *kimg, floatx4 (&sacc)[2][NT]) {
             bf16_score_init<NT>(sacc);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
@@ -1110,14 +1156,9 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64, kBf16sOccupancy<D>) void prefi
                     for (int nt = 0; nt < NT; nt++)
                         sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt], qb[nt][ks], sacc[mt][nt], 0, 0, 0);
             }
-
-            const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
-                                  (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
-            bf16x8 pb[NT];
-            bf16_softmax<NT, DT, CAP>(sacc, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo,
-                                      khi);
-
-            // O^T += V^T . P^T, and the row sums
+        };
+        // O^T += V^T . P^T, and the row sums
+        auto accumulate = [&](const uint8_t *vimg, const bf16x8 (&pb)[NT]) {
             bf16_row_sums<NT>(lacc, pb);
 #pragma unroll
             for (int t = 0; t < DT; t++) {
@@ -1126,6 +1167,42 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64, kBf16sOccupancy<D>) void prefi
                 for (int nt = 0; nt < NT; nt++)
                     o[t][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[nt], o[t][nt], 0, 0, 0);
             }
+        };
+        // The leading tiles inside the causal and window bounds of every query
+        // of the workgroup, when its waves share one query block (one q-head
+        // each): no mask, no skip test and one lazy-maximum branch per tile.
+        int n_int = 0;
+        if (p.hpw == NW) {
+            const int k_first = tfirst * KT;
+            const bool lead = k_first >= klo &&
+                              (p.sliding_window <= 0 || k_first >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
+            if (lead) n_int = max(0, min(n, (min(khi, pos0 + wq0) + 1) / KT - tfirst));
+        }
+        int i = 0;
+        for (; i < n_int; i++) {
+            arrive(i);
+            const uint8_t *kimg = ring[i % RT];
+            floatx4 sacc[2][NT];
+            scores(kimg, sacc);
+            bf16x8 pb[NT];
+            bf16_softmax_interior<NT, DT, CAP>(sacc, m, lacc, o, pb, p.softcap);
+            accumulate(kimg + 64 * D, pb);
+        }
+        for (; i < n; i++) {
+            arrive(i);
+            const int k0 = (tfirst + i) * KT;
+            // a tile wholly past this wave's last query (the causal diagonal of
+            // the workgroup's later waves) or before its window adds nothing
+            if (k0 > whi || k0 + KT - 1 < wlo) continue;
+            const uint8_t *kimg = ring[i % RT];
+            floatx4 sacc[2][NT];
+            scores(kimg, sacc);
+            const bool interior = k0 >= klo && k0 + KT - 1 <= min(khi, pos0 + wq0) &&
+                                  (p.sliding_window <= 0 || k0 >= window_lo(pos0 + wq0 + QW - 1, p.sliding_window));
+            bf16x8 pb[NT];
+            bf16_softmax<NT, DT, CAP>(sacc, m, lacc, o, pb, p.softcap, interior, k0 + 4 * lgrp, qpos, qlo, klo,
+                                      khi);
+            accumulate(kimg + 64 * D, pb);
         }
     }
 
