@@ -1073,10 +1073,13 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64, kBf16sOccupancy<D>) void prefi
         const int lq = wq0 + nt * 16 + lrow;
         const bool ok = lq < q_len;
         const float *qp = p.q + ((int64_t)(row0 + (ok ? lq : 0)) * p.n_heads + head) * D;
+        // q rows are read once per call and the output rows written once:
+        // non-temporal accesses (measured: the f32 output stream otherwise
+        // slows the q reads of the workgroups starting beside it)
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            const float4 a = *reinterpret_cast<const float4 *>(qp + ks * 32 + lgrp * 8);
-            const float4 c = *reinterpret_cast<const float4 *>(qp + ks * 32 + lgrp * 8 + 4);
+            const floatx4 a = __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(qp + ks * 32 + lgrp * 8));
+            const floatx4 c = __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(qp + ks * 32 + lgrp * 8 + 4));
             const float mul = ok ? p.q_mul : 0.0f;
             qb[nt][ks] = bf16x8{(__bf16)(a.x * mul), (__bf16)(a.y * mul), (__bf16)(a.z * mul), (__bf16)(a.w * mul),
                                 (__bf16)(c.x * mul), (__bf16)(c.y * mul), (__bf16)(c.z * mul), (__bf16)(c.w * mul)};
@@ -1232,7 +1235,7 @@ __global__ __launch_bounds__(kBf16sWaves<D> * 64, kBf16sOccupancy<D>) void prefi
             const floatx4 v = *reinterpret_cast<const floatx4 *>(stage + r * SROW + c);
             const int lq = wq0 + nt * 16 + r;
             if (lq < q_len)
-                *reinterpret_cast<floatx4 *>(p.out + ((int64_t)(row0 + lq) * p.n_heads + head) * D + c) = v;
+                __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(p.out + ((int64_t)(row0 + lq) * p.n_heads + head) * D + c));
         }
     }
 }
