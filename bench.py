@@ -546,6 +546,7 @@ PREFILL_PATTERN_MODES = {
     2: "+ f32 output stores",
     8: "+ output stores into an L2-resident 32 KB buffer",
     1: "+ f32 q loads",
+    9: "+ q loads and output stores into the L2-resident buffer",
     3: "+ q loads and output stores",
     7: "+ q loads, output stores and a minimal softmax",
 }
