@@ -529,16 +529,18 @@ def achievable(be: GpuBackend) -> dict:
     lib.glp_mfma_peak.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double)]
     nbytes = 2 << 30
     buf = be.empty(nbytes)
-    gbs, f32, bf16 = C.c_double(), C.c_double(), C.c_double()
+    gbs, f32, bf16, bf16r = C.c_double(), C.c_double(), C.c_double(), C.c_double()
     for rc in (lib.glp_stream_read(buf.ptr, nbytes, 10, C.byref(gbs)),
-               lib.glp_mfma_peak(0, 50000, C.byref(f32)), lib.glp_mfma_peak(1, 50000, C.byref(bf16))):
+               lib.glp_mfma_peak(0, 50000, C.byref(f32)), lib.glp_mfma_peak(1, 50000, C.byref(bf16)),
+               lib.glp_mfma_peak(2, 50000, C.byref(bf16r))):
         if rc != 0:
             raise RuntimeError(f"gla_probe call failed ({rc})")
     del buf
     return {"hbm_read_gbs": round(gbs.value, 1), "fp32_mfma_tflops": round(f32.value, 1),
-            "bf16_mfma_tflops": round(bf16.value, 1),
+            "bf16_mfma_tflops": round(bf16.value, 1), "bf16_mfma_random_data_tflops": round(bf16r.value, 1),
             "how": "2 GiB streaming read with non-temporal 16-byte loads; MFMA-only loops, 8 waves per CU, "
-                   "8 independent accumulators per wave (glint_amd/csrc/gla_probe.hip)"}
+                   "8 independent accumulators per wave, on near-constant operands and (bf16) on random "
+                   "N(0,1) operands (glint_amd/csrc/gla_probe.hip)"}
 
 
 PREFILL_PATTERN_MODES = {
@@ -549,6 +551,9 @@ PREFILL_PATTERN_MODES = {
     9: "+ q loads and output stores into the L2-resident buffer",
     3: "+ q loads and output stores",
     7: "+ q loads, output stores and a minimal softmax",
+    16: "mode 0 on random N(0,1) inputs (the others run on near-constant inputs)",
+    19: "mode 3 on random inputs",
+    23: "mode 7 on random inputs",
 }
 
 
@@ -734,6 +739,7 @@ def main() -> int:
             "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "timing_us": t.summary_us(),
             "frac_of_bf16_mfma_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
             "frac_of_achievable_bf16_mfma": frac_of(tf, "bf16_mfma_tflops"),
+            "frac_of_achievable_bf16_mfma_random_data": frac_of(tf, "bf16_mfma_random_data_tflops"),
             "tolerance": "max abs 3e-2 / rel 3e-2 vs the fp32 oracle (tests/test_gpu_prefill.py)"}
         if ref is not None:
             e["errors"] = error_figures(wl.gpu_sample(), ref, 3e-2, 3e-2)

@@ -67,6 +67,45 @@ __global__ __launch_bounds__(256) void mfma_bf16_kernel(int iters, float *sink) 
     if (s == 12345.0f) sink[0] = s;
 }
 
+// The bf16 loop on operands of random bits: four (A, B) register pairs per
+// lane of roughly N(0, 1) values, a different pair for each accumulator in
+// turn. The matrix units draw more power multiplying such data than the
+// near-constant operands above, and the part lowers its clock for it, so this
+// is the ceiling for attention on real activations.
+__global__ __launch_bounds__(256) void mfma_bf16_rand_kernel(int iters, float *sink) {
+    floatx4 c[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) c[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t st = 0x9e3779b9u ^ (blockIdx.x * 256 + threadIdx.x) * 0x85ebca6bu;
+    bf16x8 a[4], b[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            float x[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                // sum of four 8-bit uniforms: mean 0, variance 1 after scaling
+                st ^= st << 13;
+                st ^= st >> 17;
+                st ^= st << 5;
+                const float u = (float)(st & 255) + (float)((st >> 8) & 255) + (float)((st >> 16) & 255) +
+                                (float)(st >> 24);
+                x[h] = (u - 510.0f) * (1.0f / 147.8f);
+            }
+            a[r][k] = (__bf16)x[0];
+            b[r][k] = (__bf16)x[1];
+        }
+    for (int it = 0; it < iters; it++)
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            c[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j & 3], b[(j + 1) & 3], c[j], 0, 0, 0);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) s += c[j][0] + c[j][1] + c[j][2] + c[j][3];
+    if (s == 12345.0f) sink[0] = s;
+}
+
 // ---- the staged bf16 prefill's pattern (prefill_bf16s_kernel<128>), cfg4 grid ----
 // 32 units x 64 query blocks of 32 (longest first), 4 waves = 4 q-heads, a
 // 3-tile LDS ring of 16 KB tile images copied with global_load_lds_dwordx4
@@ -278,8 +317,8 @@ int glp_stream_read(const void *buf, size_t bytes, int reps, double *gbs_out) {
     return 0;
 }
 
-// kind 0: v_mfma_f32_16x16x4_f32, kind 1: v_mfma_f32_16x16x32_bf16, on 8
-// waves per CU; TFLOP/s.
+// kind 0: v_mfma_f32_16x16x4_f32, kind 1: v_mfma_f32_16x16x32_bf16, kind 2:
+// the bf16 loop on random operands, on 8 waves per CU; TFLOP/s.
 int glp_mfma_peak(int kind, int iters, double *tflops_out) {
     float *sink = nullptr;
     if (hipMalloc(&sink, 4) != hipSuccess) return -3;
@@ -295,8 +334,12 @@ int glp_mfma_peak(int kind, int iters, double *tflops_out) {
     if (kind == 0) {
         rc = time_ms([&] { hipLaunchKernelGGL(mfma_f32_kernel, grid, block, 0, nullptr, iters, sink); }, 3, &ms);
         flops_per_mfma = 16.0 * 16 * 4 * 2;
-    } else {
+    } else if (kind == 1) {
         rc = time_ms([&] { hipLaunchKernelGGL(mfma_bf16_kernel, grid, block, 0, nullptr, iters, sink); }, 3, &ms);
+        flops_per_mfma = 16.0 * 16 * 32 * 2;
+    } else {
+        rc = time_ms([&] { hipLaunchKernelGGL(mfma_bf16_rand_kernel, grid, block, 0, nullptr, iters, sink); }, 3,
+                     &ms);
         flops_per_mfma = 16.0 * 16 * 32 * 2;
     }
     (void)hipFree(sink);
@@ -306,8 +349,38 @@ int glp_mfma_peak(int kind, int iters, double *tflops_out) {
     return 0;
 }
 
+}  // extern "C"
+
+namespace {
+// roughly N(0, 1) from a hashed index: the sum of four 8-bit uniforms
+__device__ __forceinline__ float hashed_normal(uint32_t i) {
+    uint32_t h = i * 0x9e3779b1u;
+    h ^= h >> 15;
+    h *= 0x85ebca77u;
+    h ^= h >> 13;
+    h *= 0xc2b2ae3du;
+    h ^= h >> 16;
+    const float u = (float)(h & 255) + (float)((h >> 8) & 255) + (float)((h >> 16) & 255) + (float)(h >> 24);
+    return (u - 510.0f) * (1.0f / 147.8f);
+}
+
+// random pattern inputs: bf16 tile images of N(0, 1) values and f32 q rows of
+// N(0, 1) * q_scale (the attention kernel's q carries scale * log2(e))
+__global__ __launch_bounds__(256) void fill_random_kernel(__bf16 *img, size_t n_img, float *q, size_t n_q,
+                                                           float q_scale) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_img; i += stride)
+        img[i] = (__bf16)hashed_normal((uint32_t)i);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_q; i += stride)
+        q[i] = q_scale * hashed_normal((uint32_t)i ^ 0x5bd1e995u);
+}
+}  // namespace
+
+extern "C" {
+
 // The staged bf16 prefill's pattern over the cfg4 grid (prefill_pattern_kernel,
-// `mode` bits as above); microseconds per launch, best of `reps` single-launch
+// `mode` bits as above; bit 16: inputs of random N(0, 1) values instead of
+// near-constant ones); microseconds per launch, best of `reps` single-launch
 // timings after a warm-up.
 int glp_prefill_pattern(int mode, int reps, double *us_out) {
     const size_t img_bytes = (size_t)kPUnits * (kPQ / 32) * kPTile;
@@ -318,6 +391,11 @@ int glp_prefill_pattern(int mode, int reps, double *us_out) {
     if (hipMalloc(&img, img_bytes) != hipSuccess || hipMalloc(&q, rows_bytes) != hipSuccess ||
         hipMalloc(&out, rows_bytes) != hipSuccess) {
         rc = -3;
+    } else if (mode & 16) {
+        // q * 0.1275 = N(0, 1) rows times d^-1/2 * log2(e) at d = 128
+        hipLaunchKernelGGL(fill_random_kernel, dim3(2048), dim3(256), 0, nullptr, reinterpret_cast<__bf16 *>(img),
+                           img_bytes / 2, q, rows_bytes / sizeof(float), 0.1275f);
+        if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) rc = -3;
     } else if (hipMemset(img, 0x3c, img_bytes) != hipSuccess || hipMemset(q, 0, rows_bytes) != hipSuccess ||
                hipDeviceSynchronize() != hipSuccess) {
         rc = -3;
