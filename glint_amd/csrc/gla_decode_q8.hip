@@ -248,11 +248,14 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // no 64-bit arithmetic on the VALU.
 // The loads are non-temporal (nt): every byte is read once per call, and
 // streaming them past the caches measured ~10% faster than default loads.
+// An LDS-DMA load needs one wait state after an SALU write of M0, and the
+// compiler cannot insert it into inline assembly: hence the s_nop.
 __device__ __forceinline__ void dma16_s(const uint8_t *sbase, uint32_t voff, uint32_t m0) {
     uint32_t save;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %1, %2 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(save)
@@ -272,6 +275,7 @@ __device__ __forceinline__ void dma4_s(const uint8_t *sbase, uint32_t voff, uint
         "s_mov_b32 exec_hi, %5\n\t"
         "s_mov_b32 %1, m0\n\t"
         "s_mov_b32 m0, %6\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dword %2, %3 nt\n\t"
         "s_mov_b32 m0, %1\n\t"
         "s_mov_b64 exec, %0"

@@ -998,12 +998,14 @@ __global__ __launch_bounds__(256) void stage_bf16_kernel(const PrefillParams p, 
 
 // 16 bytes per lane from sbase + voff into LDS at m0 + 16*lane (m0 restored).
 // Default (cached) loads: each tile image is read by every query block of
-// its unit.
+// its unit. The s_nop is the wait state an LDS-DMA load needs after an SALU
+// write of M0, which the compiler cannot insert into inline assembly.
 __device__ __forceinline__ void lds_copy16(const uint8_t *sbase, uint32_t voff, uint32_t m0) {
     uint32_t save;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(save)

@@ -114,16 +114,20 @@ __global__ __launch_bounds__(256) void mfma_bf16_rand_kernel(int iters, float *s
 // O += V.P (16 MFMAs). Switches (mode bits): 1 the f32 q rows loaded and
 // converted at the start (16 KB per wave), 2 the f32 output rows stored at the
 // end (16 KB per wave, whole rows), 4 the minimal softmax, 8 the output stores
-// into one 32 KB buffer instead (L2-resident). Modes 0-9, 12 and 13. Inputs are synthetic; results
+// into one 32 KB buffer instead (L2-resident), 16 random inputs (set up by the host). Modes 0-9, 12 and 13,
+// each with or without 16. Inputs are synthetic; results
 // are discarded. Every access is in bounds: the images are 32 x 64 tiles, q and
 // out 32 x 4 x 2048 rows of 128 floats.
 constexpr int kPD = 128, kPTile = 128 * kPD, kPRing = 3, kPUnits = 32, kPQ = 2048;
 
+// as the kernel's lds_copy16 (the s_nop: an LDS-DMA load's wait state after an
+// SALU write of M0)
 __device__ __forceinline__ void p_lds_copy16(const uint8_t *sbase, uint32_t voff, uint32_t m0) {
     uint32_t save;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(save)
