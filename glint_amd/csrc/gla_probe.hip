@@ -106,6 +106,35 @@ __global__ __launch_bounds__(256) void mfma_bf16_rand_kernel(int iters, float *s
     if (s == 12345.0f) sink[0] = s;
 }
 
+// The fp32 loop on random N(0, 1) operands (as mfma_bf16_rand_kernel).
+__global__ __launch_bounds__(256) void mfma_f32_rand_kernel(int iters, float *sink) {
+    floatx4 c[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) c[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t st = 0x9e3779b9u ^ (blockIdx.x * 256 + threadIdx.x) * 0x85ebca6bu;
+    float a[4], b[4];
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        st ^= st << 13;
+        st ^= st >> 17;
+        st ^= st << 5;
+        const float u =
+            (float)(st & 255) + (float)((st >> 8) & 255) + (float)((st >> 16) & 255) + (float)(st >> 24);
+        const float x = (u - 510.0f) * (1.0f / 147.8f);
+        if (r < 4)
+            a[r] = x;
+        else
+            b[r - 4] = x;
+    }
+    for (int it = 0; it < iters; it++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) c[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j & 3], b[(j + 1) & 3], c[j], 0, 0, 0);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) s += c[j][0] + c[j][1] + c[j][2] + c[j][3];
+    if (s == 12345.0f) sink[0] = s;
+}
+
 // ---- the staged bf16 prefill's pattern (prefill_bf16s_kernel<128>), cfg4 grid ----
 // 32 units x 64 query blocks of 32 (longest first), 4 waves = 4 q-heads, a
 // 3-tile LDS ring of 16 KB tile images copied with global_load_lds_dwordx4
@@ -322,7 +351,8 @@ int glp_stream_read(const void *buf, size_t bytes, int reps, double *gbs_out) {
 }
 
 // kind 0: v_mfma_f32_16x16x4_f32, kind 1: v_mfma_f32_16x16x32_bf16, kind 2:
-// the bf16 loop on random operands, on 8 waves per CU; TFLOP/s.
+// the bf16 loop on random operands, kind 3: the fp32 loop on random operands,
+// on 8 waves per CU; TFLOP/s.
 int glp_mfma_peak(int kind, int iters, double *tflops_out) {
     float *sink = nullptr;
     if (hipMalloc(&sink, 4) != hipSuccess) return -3;
@@ -341,10 +371,14 @@ int glp_mfma_peak(int kind, int iters, double *tflops_out) {
     } else if (kind == 1) {
         rc = time_ms([&] { hipLaunchKernelGGL(mfma_bf16_kernel, grid, block, 0, nullptr, iters, sink); }, 3, &ms);
         flops_per_mfma = 16.0 * 16 * 32 * 2;
-    } else {
+    } else if (kind == 2) {
         rc = time_ms([&] { hipLaunchKernelGGL(mfma_bf16_rand_kernel, grid, block, 0, nullptr, iters, sink); }, 3,
                      &ms);
         flops_per_mfma = 16.0 * 16 * 32 * 2;
+    } else {
+        rc = time_ms([&] { hipLaunchKernelGGL(mfma_f32_rand_kernel, grid, block, 0, nullptr, iters, sink); }, 3,
+                     &ms);
+        flops_per_mfma = 16.0 * 16 * 4 * 2;
     }
     (void)hipFree(sink);
     if (rc != 0) return rc;
