@@ -108,6 +108,49 @@ def test_prefill_bf16_varlen_batch(backend, dtype, d, H, Hkv):
 
 
 @pytest.mark.parametrize("precision", ["f32", "bf16"])
+def test_prefill_zero_length_prompts(backend, precision):
+    """Prompts with no tokens between and around others in one launch (chunked prefill can hand
+    a sequence an empty chunk): the others' rows are unaffected."""
+    H, Hkv, d = 8, 2, 128
+    lens = [0, 45, 0, 7, 0]
+    offs = [5, 0, 30, 60, 0]
+    max_seq = max(o + n for o, n in zip(offs, lens)) + 8
+    c = Contig(backend, "f32", len(lens), 1, max_seq, Hkv, d, seed=611)
+    q = synth.normal(612, (sum(lens), H, d))
+    q_start = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    tol = (BF16_ABS_TOL, BF16_REL_TOL) if precision == "bf16" else ()
+    for cap, window in [(None, None), (25.0, 20)]:
+        got = run_prefill(backend, c.cache, q, q_start, offs, H, 0.088, cap, window, precision=precision)
+        for b in range(len(lens)):
+            if lens[b] == 0:
+                continue
+            rows = slice(q_start[b], q_start[b + 1])
+            want = _oracle_prefill(c.stores[b], q[rows], offs[b], H, Hkv, d, 0.088, cap, window)
+            assert_close(got[rows], want, *tol, what=f"{precision} seq {b} cap {cap} w {window}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+def test_prefill_bf16_d256_long_prompt(backend, monkeypatch, dtype):
+    """head_dim 256 (the 4-tile ring: two tiles in flight behind the current one) over a long
+    chunk: 700 queries after 100 cached positions, 25 tiles per query block at the end; with
+    and without soft-cap and window, against the oracle at the bf16 bar and bit-identical to
+    the per-workgroup path."""
+    H, Hkv, d = 8, 4, 256
+    lens, offs = [700], [100]
+    c = Contig(backend, dtype, 1, 1, 800, Hkv, d, seed=2560)
+    q = synth.normal(2561, (700, H, d))
+    q_start = np.array([0, 700], np.int32)
+    for cap, window in [(None, None), (50.0, None), (None, 300)]:
+        monkeypatch.delenv("GLA_BF16_UNSTAGED", raising=False)
+        got = run_prefill(backend, c.cache, q, q_start, offs, H, 0.0625, cap, window, precision="bf16")
+        want = _oracle_prefill(c.stores[0], q, 100, H, Hkv, d, 0.0625, cap, window)
+        assert_close(got, want, BF16_ABS_TOL, BF16_REL_TOL, what=f"{dtype} d256 cap {cap} w {window}")
+        monkeypatch.setenv("GLA_BF16_UNSTAGED", "1")
+        unstaged = run_prefill(backend, c.cache, q, q_start, offs, H, 0.0625, cap, window, precision="bf16")
+        assert np.array_equal(got.view(np.uint32), unstaged.view(np.uint32)), (dtype, cap, window)
+
+
+@pytest.mark.parametrize("precision", ["f32", "bf16"])
 def test_prefill_indexing_is_bit_exact(backend, precision):
     """K = 0 and small-integer V: out = mean of V over [window(pos), pos] exactly."""
     H, Hkv, d = 8, 2, 64
