@@ -156,12 +156,16 @@ __device__ __forceinline__ void fetch_tile(const PrefillParams &p, int b, int kv
                 }
             } else {
                 const int64_t base = pid * p.kv.page_stride + head_off + (int64_t)slot * p.kv.row_stride;
-                const float4 *kp4 = reinterpret_cast<const float4 *>(p.kv.k + base) + c16 * 4;
-                const float4 *vp4 = reinterpret_cast<const float4 *>(p.kv.v + base) + c16 * 4;
+                // chunk q of the lane: floats 4*c16 + q*D/4 of the row, so
+                // each load and each LDS store instruction covers whole
+                // 128-byte runs of a row (16 consecutive floats per lane
+                // made the LDS stores conflict)
+                const float4 *kp4 = reinterpret_cast<const float4 *>(p.kv.k + base) + c16;
+                const float4 *vp4 = reinterpret_cast<const float4 *>(p.kv.v + base) + c16;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    t.k[j][q] = kp4[q];
-                    t.v[j][q] = vp4[q];
+                    t.k[j][q] = kp4[q * (D / 16)];
+                    t.v[j][q] = vp4[q * (D / 16)];
                 }
                 continue;
             }
@@ -185,7 +189,7 @@ __device__ __forceinline__ void fetch_tile(const PrefillParams &p, int b, int kv
 template <int D>
 constexpr int kRow = D + 4;
 
-template <int D, int NTHR>
+template <int D, int NTHR, bool Q8>
 __device__ __forceinline__ void store_tile(const TileRegs<D, NTHR> &t, float *Ks, float *Vs) {
 #pragma unroll
     for (int j = 0; j < TileRegs<D, NTHR>::PER_THREAD; j++) {
@@ -193,12 +197,13 @@ __device__ __forceinline__ void store_tile(const TileRegs<D, NTHR> &t, float *Ks
         if (u >= TileRegs<D, NTHR>::UNITS) break;
         const int key = u / (D / 16);
         const int c16 = u - key * (D / 16);
-        float4 *kd = reinterpret_cast<float4 *>(Ks + key * kRow<D> + c16 * 16);
-        float4 *vd = reinterpret_cast<float4 *>(Vs + key * kRow<D> + c16 * 16);
+        // chunk q: floats 16*c16 + 4*q of the row (Q8) or 4*c16 + q*D/4 (f32)
+        float4 *kd = reinterpret_cast<float4 *>(Ks + key * kRow<D> + (Q8 ? c16 * 16 : c16 * 4));
+        float4 *vd = reinterpret_cast<float4 *>(Vs + key * kRow<D> + (Q8 ? c16 * 16 : c16 * 4));
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            kd[q] = t.k[j][q];
-            vd[q] = t.v[j][q];
+            kd[Q8 ? q : q * (D / 16)] = t.k[j][q];
+            vd[Q8 ? q : q * (D / 16)] = t.v[j][q];
         }
     }
 }
@@ -292,7 +297,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_f32_kernel(const PrefillParam
         const int kfirst = (klo / KT) * KT;
         TileRegs<D, NTHR> tr;
         fetch_tile<D, NTHR, Q8>(p, b, kvh, kfirst, klo, khi, tr);
-        store_tile<D, NTHR>(tr, Ks[0], Vs[0]);
+        store_tile<D, NTHR, Q8>(tr, Ks[0], Vs[0]);
         __syncthreads();
         int buf = 0;
         for (int k0 = kfirst; k0 <= khi; k0 += KT, buf ^= 1) {
@@ -395,7 +400,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_f32_kernel(const PrefillParam
                 }
             }
 
-            if (more) store_tile<D, NTHR>(tr, Ks[buf ^ 1], Vs[buf ^ 1]);
+            if (more) store_tile<D, NTHR, Q8>(tr, Ks[buf ^ 1], Vs[buf ^ 1]);
             __syncthreads();
         }
     }
