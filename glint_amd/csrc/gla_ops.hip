@@ -336,11 +336,17 @@ __global__ __launch_bounds__(kSkWaves * 64) void matvec_q8_splitk_kernel(
     }
 
     // merge the waves' block ranges in a fixed order
-    __shared__ floatx4 red[kSkWaves][RT * NVT][64];
+    // (through LDS with padding: 4 floats after every 16 lanes, and tiles of
+    // S floats with NVT * S = 16 (mod 64), so that the 64 reads of one wave
+    // below, 4 row tiles x 4 lane groups x 4 registers, fall in distinct banks)
+    constexpr int S = NVT == 1 ? 272 : (NVT == 2 ? 296 : (NVT == 3 ? 304 : 276));
+    static_assert((NVT * S) % 64 == 16 && 4 * 63 + 4 * 3 + 3 < S && S % 4 == 0, "padded tile");
+    __shared__ __attribute__((aligned(16))) float red[kSkWaves * RT * NVT * S];
+    auto red_at = [&](int w, int rt, int vt, int ln) { return ((w * RT + rt) * NVT + vt) * S + 4 * ln + 4 * (ln >> 4); };
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-        for (int vt = 0; vt < NVT; vt++) red[wave][rt * NVT + vt][lane] = acc[rt][vt];
+        for (int vt = 0; vt < NVT; vt++) *reinterpret_cast<floatx4 *>(&red[red_at(wave, rt, vt, lane)]) = acc[rt][vt];
     __syncthreads();
     float *o = out + (int64_t)blockIdx.y * split_stride;
     for (int i = threadIdx.x; i < RT * 16 * NVT * 16; i += kSkWaves * 64) {
@@ -351,9 +357,9 @@ __global__ __launch_bounds__(kSkWaves * 64) void matvec_q8_splitk_kernel(
         const int vt = vv >> 4;
         const int ln = (rr >> 2) * 16 + (vv & 15);  // the C lane of (row rr, vector vv & 15)
         const int r = rr & 3;
-        float sum = red[0][rt * NVT + vt][ln][r];
+        float sum = red[red_at(0, rt, vt, ln) + r];
 #pragma unroll
-        for (int w = 1; w < kSkWaves; w++) sum += red[w][rt * NVT + vt][ln][r];
+        for (int w = 1; w < kSkWaves; w++) sum += red[red_at(w, rt, vt, ln) + r];
         const int row = tile0 * 16 + rl;
         const int v = v0 + vv;
         if (row < rows && v < n_vec) o[(int64_t)vv * rows + row] = sum * xsl[vv];
