@@ -1,0 +1,104 @@
+"""A seeded sweep over shapes the hand-picked tests do not name: prefill (fp32 and bf16-input) and
+decode against the oracle (src/transformer/forward.rs:927-958 prefill loop, :1468-1507 batched
+decode, flash.rs:46-124 per head) with head_dim 64/128/256, GQA groups 1-8, empty and ragged
+lengths, arbitrary chunk offsets and window starts, soft-cap and sliding window on or off, f32
+and Q8_0 caches. Every case is drawn from its own fixed seed, so a failure names a reproducible
+shape. Bars: fp32 abs 1e-4 / rel 1e-3; bf16-input prefill abs 3e-2 / rel 3e-2 against the fp32
+oracle (helpers.py), and bit-identical to the per-workgroup bf16 path."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from glint_amd import synth
+from gpu_util import Contig, run_decode, run_prefill
+from helpers import BF16_ABS_TOL, BF16_REL_TOL, assert_close
+
+pytestmark = pytest.mark.gpu
+
+N_PREFILL = 32
+N_DECODE = 32
+
+
+def _prefill_case(i):
+    rng = np.random.default_rng(91000 + i)
+    d = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2, 4]))
+    group = int(rng.choice([1, 2, 3, 4, 8]))
+    n_seqs = int(rng.integers(1, 4))
+    lens = [int(x) for x in rng.integers(0, 261, n_seqs)]
+    if sum(lens) == 0:
+        lens[0] = int(rng.integers(1, 100))
+    offs = [int(x) for x in rng.integers(0, 151, n_seqs)]
+    window = None if rng.random() < 0.5 else int(rng.integers(1, 301))
+    cap = None if rng.random() < 0.5 else float(rng.uniform(5.0, 60.0))
+    dtype = str(rng.choice(["f32", "q8"]))
+    precision = str(rng.choice(["f32", "bf16"]))
+    # the bf16 bar is stated for unit-scale scores; the fp32 path also takes other scales
+    scale = float(1.0 / np.sqrt(d)) * (1.0 if precision == "bf16" else float(rng.uniform(0.5, 2.0)))
+    extra = int(rng.integers(0, 41))
+    return dict(d=d, hkv=hkv, H=hkv * group, lens=lens, offs=offs, window=window, cap=cap, dtype=dtype,
+                precision=precision, scale=scale, max_seq=max(o + n for o, n in zip(offs, lens)) + extra)
+
+
+def _decode_case(i):
+    rng = np.random.default_rng(92000 + i)
+    d = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 4, 8]))
+    B = int(rng.integers(1, 9))
+    total = [int(x) for x in rng.integers(1, 3001, B)]
+    # a window start anywhere in the sequence (the length attended is what follows it); some
+    # sequences attend nothing
+    starts = [int(rng.integers(0, t)) if rng.random() < 0.5 else 0 for t in total]
+    lens = [t - s for t, s in zip(total, starts)]
+    if B > 1 and rng.random() < 0.3:
+        lens[int(rng.integers(0, B))] = 0
+    cap = None if rng.random() < 0.5 else float(rng.uniform(5.0, 60.0))
+    dtype = str(rng.choice(["f32", "q8"]))
+    scale = float(1.0 / np.sqrt(d)) * float(rng.uniform(0.5, 2.0))
+    return dict(d=d, hkv=hkv, H=hkv * group, starts=starts, lens=lens, cap=cap, dtype=dtype, scale=scale,
+                max_seq=max(total))
+
+
+@pytest.mark.parametrize("case", range(N_PREFILL))
+def test_prefill_random_shapes(backend, monkeypatch, case):
+    c_ = _prefill_case(case)
+    d, hkv, H = c_["d"], c_["hkv"], c_["H"]
+    lens, offs = c_["lens"], c_["offs"]
+    c = Contig(backend, c_["dtype"], len(lens), 1, c_["max_seq"], hkv, d, seed=93000 + case)
+    q = synth.normal(94000 + case, (sum(lens), H, d))
+    q_start = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    monkeypatch.delenv("GLA_BF16_UNSTAGED", raising=False)
+    got = run_prefill(backend, c.cache, q, q_start, offs, H, c_["scale"], c_["cap"], c_["window"],
+                      precision=c_["precision"])
+    tol = (BF16_ABS_TOL, BF16_REL_TOL) if c_["precision"] == "bf16" else ()
+    for b, n in enumerate(lens):
+        if n == 0:
+            continue
+        rows = slice(q_start[b], q_start[b + 1])
+        want = orc.prefill(q[rows].reshape(n, H * d), c.stores[b], 0, offs[b], H, hkv, d, c_["scale"], c_["cap"],
+                           c_["window"]).reshape(n, H, d)
+        assert_close(got[rows], want, *tol, what=f"case {case} {c_} seq {b}")
+    if c_["precision"] == "bf16":
+        monkeypatch.setenv("GLA_BF16_UNSTAGED", "1")
+        unstaged = run_prefill(backend, c.cache, q, q_start, offs, H, c_["scale"], c_["cap"], c_["window"],
+                               precision="bf16")
+        assert np.array_equal(got.view(np.uint32), unstaged.view(np.uint32)), (case, c_)
+
+
+@pytest.mark.parametrize("case", range(N_DECODE))
+def test_decode_random_shapes(backend, case):
+    c_ = _decode_case(case)
+    d, hkv, H = c_["d"], c_["hkv"], c_["H"]
+    starts = np.asarray(c_["starts"], np.int32)
+    lens = np.asarray(c_["lens"], np.int32)
+    B = len(lens)
+    c = Contig(backend, c_["dtype"], B, 1, c_["max_seq"], hkv, d, seed=95000 + case)
+    q = synth.normal(96000 + case, (B, H, d))
+    want = orc.decode_batch(q.reshape(B, H * d), c.stores, 0, starts, lens, H, hkv, d, c_["scale"],
+                            c_["cap"]).reshape(B, H, d)
+    for host_lengths in (True, False):
+        got = run_decode(backend, c.cache, q, starts, lens, H, c_["scale"], c_["cap"], host_lengths=host_lengths)
+        assert_close(got, want, what=f"case {case} {c_} host lengths {host_lengths}")
