@@ -2,7 +2,8 @@
 decode against the oracle (src/transformer/forward.rs:927-958 prefill loop, :1468-1507 batched
 decode, flash.rs:46-124 per head) with head_dim 64/128/256, GQA groups 1-8, empty and ragged
 lengths, arbitrary chunk offsets and window starts, soft-cap and sliding window on or off, f32
-and Q8_0 caches. Every case is drawn from its own fixed seed, so a failure names a reproducible
+and Q8_0 caches, contiguous and paged (permuted page tables with a shared prefix). Every case
+is drawn from its own fixed seed, so a failure names a reproducible
 shape. Bars: fp32 abs 1e-4 / rel 1e-3; bf16-input prefill abs 3e-2 / rel 3e-2 against the fp32
 oracle (helpers.py), and bit-identical to the per-workgroup bf16 path."""
 from __future__ import annotations
@@ -12,13 +13,14 @@ import pytest
 
 import oracle as orc
 from glint_amd import synth
-from gpu_util import Contig, run_decode, run_prefill
+from gpu_util import Contig, Pool, run_decode, run_prefill
 from helpers import BF16_ABS_TOL, BF16_REL_TOL, assert_close
 
 pytestmark = pytest.mark.gpu
 
 N_PREFILL = 32
 N_DECODE = 32
+N_PAGED = 16
 
 
 def _prefill_case(i):
@@ -102,3 +104,59 @@ def test_decode_random_shapes(backend, case):
     for host_lengths in (True, False):
         got = run_decode(backend, c.cache, q, starts, lens, H, c_["scale"], c_["cap"], host_lengths=host_lengths)
         assert_close(got, want, what=f"case {case} {c_} host lengths {host_lengths}")
+
+
+def _paged_case(i):
+    rng = np.random.default_rng(97000 + i)
+    d = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 4, 8]))
+    B = int(rng.integers(1, 9))
+    ctx = [int(x) for x in rng.integers(1, 2001, B)]
+    prefix = int(rng.choice([0, 16, 64, 200]))
+    window = None if rng.random() < 0.5 else int(rng.integers(1, 700))
+    cap = None if rng.random() < 0.5 else float(rng.uniform(5.0, 60.0))
+    dtype = str(rng.choice(["f32", "q8"]))
+    scale = float(1.0 / np.sqrt(d)) * float(rng.uniform(0.5, 2.0))
+    # prefill: each sequence prefills its last n positions (the first ones are "cached")
+    n_new = [int(rng.integers(0, min(c, 200) + 1)) for c in ctx]
+    precision = str(rng.choice(["f32", "bf16"]))
+    return dict(d=d, hkv=hkv, H=hkv * group, ctx=ctx, prefix=prefix, window=window, cap=cap, dtype=dtype,
+                scale=scale, n_new=n_new, precision=precision)
+
+
+@pytest.mark.parametrize("case", range(N_PAGED))
+def test_paged_random_shapes(backend, case):
+    """Decode and chunked prefill over one paged pool: the sequences' tables share a prefix and
+    map logical pages to a seeded permutation of physical ones."""
+    c_ = _paged_case(case)
+    d, hkv, H = c_["d"], c_["hkv"], c_["H"]
+    ctx = np.asarray(c_["ctx"], np.int32)
+    pb = synth.paged_batch(98000 + case, ctx, prefix_tokens=c_["prefix"])
+    p = Pool(backend, c_["dtype"], pb, hkv, d, seed=99000 + case)
+    B = len(ctx)
+    # decode at position ctx - 1 over the window
+    w = synth.windowed(pb, c_["window"])
+    q = synth.normal(99500 + case, (B, H, d))
+    want = orc.decode_batch(q.reshape(B, H * d), p.stores, 0, w.kv_start, w.kv_len, H, hkv, d, c_["scale"],
+                            c_["cap"]).reshape(B, H, d)
+    got = run_decode(backend, p.pool, q, w.kv_start, w.kv_len, H, c_["scale"], c_["cap"], table=pb.table)
+    assert_close(got, want, what=f"case {case} {c_} decode")
+    # chunked prefill of each sequence's last n_new positions
+    n = np.asarray(c_["n_new"], np.int32)
+    if n.sum() == 0:
+        return
+    scale = float(1.0 / np.sqrt(d)) if c_["precision"] == "bf16" else c_["scale"]
+    offs = ctx - n
+    qp = synth.normal(99700 + case, (int(n.sum()), H, d))
+    q_start = np.concatenate([[0], np.cumsum(n)]).astype(np.int32)
+    got = run_prefill(backend, p.pool, qp, q_start, offs, H, scale, c_["cap"], c_["window"], table=pb.table,
+                      precision=c_["precision"])
+    tol = (BF16_ABS_TOL, BF16_REL_TOL) if c_["precision"] == "bf16" else ()
+    for b in range(B):
+        if n[b] == 0:
+            continue
+        rows = slice(q_start[b], q_start[b + 1])
+        want = orc.prefill(qp[rows].reshape(int(n[b]), H * d), p.stores[b], 0, int(offs[b]), H, hkv, d, scale,
+                           c_["cap"], c_["window"]).reshape(int(n[b]), H, d)
+        assert_close(got[rows], want, *tol, what=f"case {case} {c_} prefill seq {b}")
