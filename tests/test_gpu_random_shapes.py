@@ -2,7 +2,8 @@
 decode against the oracle (src/transformer/forward.rs:927-958 prefill loop, :1468-1507 batched
 decode, flash.rs:46-124 per head) with head_dim 64/128/256, GQA groups 1-8, empty and ragged
 lengths, arbitrary chunk offsets and window starts, soft-cap and sliding window on or off, f32
-and Q8_0 caches, contiguous and paged (permuted page tables with a shared prefix). Every case
+and Q8_0 caches, contiguous and paged (permuted page tables with a shared prefix); and the Q8_0 matvec
+(quantized.rs:247-346) over vector counts, row counts, widths and x alignments. Every case
 is drawn from its own fixed seed, so a failure names a reproducible
 shape. Bars: fp32 abs 1e-4 / rel 1e-3; bf16-input prefill abs 3e-2 / rel 3e-2 against the fp32
 oracle (helpers.py), and bit-identical to the per-workgroup bf16 path."""
@@ -160,3 +161,53 @@ def test_paged_random_shapes(backend, case):
         want = orc.prefill(qp[rows].reshape(int(n[b]), H * d), p.stores[b], 0, int(offs[b]), H, hkv, d, scale,
                            c_["cap"], c_["window"]).reshape(int(n[b]), H, d)
         assert_close(got[rows], want, *tol, what=f"case {case} {c_} prefill seq {b}")
+
+
+N_MATVEC = 24
+
+
+def _matvec_case(i):
+    rng = np.random.default_rng(99800 + i)
+    rows = int(rng.integers(1, 701))
+    cols = 32 * int(rng.integers(1, 601))     # past 16,384 the activation split reads each row twice
+    n_vec = int(rng.integers(1, 5)) if rng.random() < 0.3 else int(rng.integers(5, 151))
+    misaligned = bool(rng.random() < 0.5)       # x 4 bytes past a 16-byte boundary: scalar loads
+    return dict(rows=rows, cols=cols, n_vec=n_vec, misaligned=misaligned)
+
+
+class _At:
+    """A device pointer `offset` bytes into a buffer (the matvec reads only `.ptr`)."""
+
+    def __init__(self, buf, offset):
+        import ctypes
+        self.ptr = ctypes.c_void_p(buf.ptr.value + offset)
+
+
+@pytest.mark.parametrize("case", range(N_MATVEC))
+def test_matvec_random_shapes(backend, case):
+    """Q8_0 matvec (src/tensor/quantized.rs:247-346, :587-610) over seeded shapes: the vector-ALU
+    kernel for 1-4 vectors, the split-K MFMA kernel with 1-4 vector tiles per launch and several
+    launches, row tails, odd block counts and x at any 4-byte alignment. Bar as in the ops tests:
+    |got - f64| <= 2e-6 x sum_c |w x|, and the oracle within 4e-6 of the same sum."""
+    c_ = _matvec_case(case)
+    rows, cols, n_vec = c_["rows"], c_["cols"], c_["n_vec"]
+    raw = orc.q8_quantize_rows(synth.normal_rows(99900 + case, rows, cols)).reshape(-1)
+    x = synth.normal(99950 + case, (n_vec, cols))
+    x[:, : 1 + case % 5] *= 300.0   # a few large entries: each vector's piece scale follows its largest
+    w = backend.create_q8_weights(raw, rows, cols)
+    pad = 1 if c_["misaligned"] else 0
+    dx = backend.buffer(np.concatenate([np.zeros(pad, np.float32), x.reshape(-1)]))
+    dy = backend.empty(n_vec * rows * 4)
+    backend.matvec_q8_0(w, _At(dx, 4 * pad), n_vec, dy)
+    backend.sync()
+    got = dy.download((n_vec, rows))
+    w.destroy()
+    blk = raw.reshape(rows, cols // 32, 34)
+    wd = (blk[:, :, 2:].view(np.int8).astype(np.float64) *
+          blk[:, :, :2].copy().view("<f2").astype(np.float64)).reshape(rows, cols)
+    exact = x.astype(np.float64) @ wd.T
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wd).T
+    assert np.all(np.abs(got - exact) <= 2e-6 * mag), (case, c_, float(np.max(np.abs(got - exact) / mag)))
+    for v in sorted({0, n_vec // 2, n_vec - 1}):
+        want = orc.matvec_q8_0(raw, rows, cols, x[v])
+        assert np.all(np.abs(got[v] - want) <= 4e-6 * mag[v]), (case, c_, v)
