@@ -142,6 +142,11 @@ struct gla_ctx {
     // after its context frees only itself.
     std::vector<gla_kv *> kvs;
     std::vector<gla_q8w *> q8ws;
+    // RoPE inverse frequencies 1 / powf(base, 2p / head_dim) of the last
+    // (base, head_dim) rotated on this context, computed on the host
+    float rope_base = 0.0f;
+    int rope_head_dim = 0;
+    std::vector<float> rope_freq;
 };
 
 struct gla_kv {

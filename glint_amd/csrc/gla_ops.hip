@@ -27,6 +27,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <string.h>
 
 #include <algorithm>
 #include <vector>
@@ -61,11 +62,23 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // ---- RoPE -----------------------------------------------------------------
 
-// One thread per (row, head, pair): the pair (i, i+1), i even and below
-// rot = min(rot_dim, head_dim) & ~1, rotated by (pos / scaling) * base^(-i/d),
-// with the reference's f32 operations in its order and no contraction.
-__global__ __launch_bounds__(256) void rope_kernel(float *x, int n_rows, int n_heads, int head_dim, int n_pairs,
-                                                   const int32_t *pos, float freq_base, float scaling_factor) {
+// The frequencies of up to kRopeLaunchPairs pairs, passed by value (1 KiB of
+// kernel arguments: no device buffer, nothing to copy before the launch).
+constexpr int kRopeLaunchPairs = 256;
+struct RopeFreqs {
+    float f[kRopeLaunchPairs];
+};
+
+// One thread per (row, head, pair) of the launch's pairs p0 .. p0 + n_pairs:
+// the pair (i, i+1), i = 2 * pair, rotated by (pos / scaling) * freq, with
+// the reference's f32 operations in its order and no contraction. freq =
+// 1 / powf(base, i / d) comes from the host's powf, the libm routine the
+// reference's f32::powf calls, because that powf is not correctly rounded for
+// every argument (a device pow rounded to f32 differs from it in about one
+// case in a thousand, and the angle then differs by an ulp times pos).
+__global__ __launch_bounds__(256) void rope_kernel(float *x, int n_rows, int n_heads, int head_dim, int p0,
+                                                   int n_pairs, const int32_t *pos, float scaling_factor,
+                                                   RopeFreqs fr) {
 #pragma clang fp contract(off)
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t total = (int64_t)n_rows * n_heads * n_pairs;
@@ -73,14 +86,9 @@ __global__ __launch_bounds__(256) void rope_kernel(float *x, int n_rows, int n_h
     const int pr = (int)(t % n_pairs);
     const int64_t rh = t / n_pairs;
     const int row = (int)(rh / n_heads);
-    const int i = 2 * pr;
+    const int i = 2 * (p0 + pr);
     const float pos_scaled = (float)pos[row] / scaling_factor;
-    // base^(i/d) correctly rounded to f32 (through double precision), which
-    // is what glibc's powf returns for these arguments, then the reference's
-    // f32 reciprocal: the angles, and so the rotations, match it bit for bit
-    // up to cos/sin's last-place differences
-    const float pw = (float)pow((double)freq_base, (double)((float)i / (float)head_dim));
-    const float freq = 1.0f / pw;
+    const float freq = fr.f[pr];
     const float angle = pos_scaled * freq;
     const float c = cosf(angle);
     const float s = sinf(angle);
@@ -611,11 +619,26 @@ int gla_rope(gla_ctx *ctx, float *x, int n_rows, int n_heads, int head_dim, cons
     const int n_pairs = rot / 2;
     if (n_rows == 0 || n_pairs == 0) return GLA_OK;
     GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
-    const int64_t total = (int64_t)n_rows * n_heads * n_pairs;
-    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)grid_for(total)), dim3(256), 0, ctx->stream, x, n_rows, n_heads,
-                       head_dim, n_pairs, pos, freq_base, scaling_factor);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "rope_kernel launch: %s", hipGetErrorString(e));
+    // the context keeps the table of the last (base, head_dim): a model's
+    // layers all rotate with the same one
+    std::vector<float> &tab = ctx->rope_freq;
+    if (memcmp(&ctx->rope_base, &freq_base, sizeof(float)) != 0 || ctx->rope_head_dim != head_dim ||
+        (int)tab.size() < n_pairs) {
+        tab.resize(n_pairs);
+        for (int p = 0; p < n_pairs; p++) tab[p] = 1.0f / powf(freq_base, (float)(2 * p) / (float)head_dim);
+        ctx->rope_base = freq_base;
+        ctx->rope_head_dim = head_dim;
+    }
+    for (int p0 = 0; p0 < n_pairs; p0 += kRopeLaunchPairs) {
+        const int np = std::min(kRopeLaunchPairs, n_pairs - p0);
+        RopeFreqs fr;
+        for (int p = 0; p < kRopeLaunchPairs; p++) fr.f[p] = p < np ? tab[p0 + p] : 0.0f;
+        const int64_t total = (int64_t)n_rows * n_heads * np;
+        hipLaunchKernelGGL(rope_kernel, dim3((unsigned)grid_for(total)), dim3(256), 0, ctx->stream, x, n_rows, n_heads,
+                           head_dim, p0, np, pos, scaling_factor, fr);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "rope_kernel launch: %s", hipGetErrorString(e));
+    }
     return GLA_OK;
 }
 

@@ -263,9 +263,11 @@ int gla_attention_resident(gla_ctx *ctx, const float *q, const gla_kv *cache, in
 /* RoPE in place, ops::rope (src/tensor/ops.rs:212-245) on device rows:
  * x [n_rows][n_heads][head_dim], row r at position pos[r] (device int32).
  * For even i < min(rot_dim, head_dim) & ~1 every head's pair (i, i+1) is
- * rotated by (pos / scaling_factor) * freq_base^(-i / head_dim); the other
- * dimensions are left as they are. Like the reference, freq_base and
- * scaling_factor are not validated. Asynchronous. */
+ * rotated by (pos / scaling_factor) * (1 / powf(freq_base, i / head_dim)),
+ * the frequency taken from the host's powf as the reference's f32::powf
+ * takes it; the other dimensions are left as they are. Like the reference,
+ * freq_base and scaling_factor are not validated. Asynchronous; no device
+ * allocation or copy (the frequencies travel as kernel arguments). */
 int gla_rope(gla_ctx *ctx, float *x, int n_rows, int n_heads, int head_dim, const int32_t *pos, float freq_base,
              float scaling_factor, int rot_dim);
 

@@ -46,6 +46,8 @@ def test_rope_reference_known_answers(backend):
     (9, 64, 64, 10000.0, 1.0),       # SmolLM
     (4, 96, 48, 10000.0, 4.0),       # Phi-3-style partial rotary, linear scaling
     (2, 64, 33, 10000.0, 1.0),       # odd rot_dim rounds down
+    (2, 1100, 1100, 10000.0, 1.0),   # 550 pairs: three launches of at most 256 pairs
+    (3, 251, 251, 10000.0, 1.0),     # glibc's powf is not correctly rounded at i = 110 here
 ])
 def test_rope_matches_oracle(backend, n_heads, head_dim, rot_dim, base, scaling):
     pos = np.array([0, 1, 17, 511, 4095, 8191, 65535], np.int32)

@@ -3,7 +3,8 @@ decode against the oracle (src/transformer/forward.rs:927-958 prefill loop, :146
 decode, flash.rs:46-124 per head) with head_dim 64/128/256, GQA groups 1-8, empty and ragged
 lengths, arbitrary chunk offsets and window starts, soft-cap and sliding window on or off, f32
 and Q8_0 caches, contiguous and paged (permuted page tables with a shared prefix); and the Q8_0 matvec
-(quantized.rs:247-346) over vector counts, row counts, widths and x alignments. Every case
+(quantized.rs:247-346) over vector counts, row counts, widths and x alignments, and RoPE
+(ops.rs:212-245) over head and rotary dimensions, bases, scalings and positions. Every case
 is drawn from its own fixed seed, so a failure names a reproducible
 shape. Bars: fp32 abs 1e-4 / rel 1e-3; bf16-input prefill abs 3e-2 / rel 3e-2 against the fp32
 oracle (helpers.py), and bit-identical to the per-workgroup bf16 path."""
@@ -211,3 +212,35 @@ def test_matvec_random_shapes(backend, case):
     for v in sorted({0, n_vec // 2, n_vec - 1}):
         want = orc.matvec_q8_0(raw, rows, cols, x[v])
         assert np.all(np.abs(got[v] - want) <= 4e-6 * mag[v]), (case, c_, v)
+
+
+N_ROPE = 16
+
+
+@pytest.mark.parametrize("case", range(N_ROPE))
+def test_rope_random_shapes(backend, case):
+    """RoPE (src/tensor/ops.rs:212-245) over seeded head counts, head and rotary dimensions (odd
+    ones included), bases, linear scalings and positions up to 2^20; the dimensions past the
+    rotary part are left bit for bit. Bar: max abs 1e-5 x max|x| per row, as in the ops tests."""
+    rng = np.random.default_rng(99600 + case)
+    head_dim = int(rng.integers(1, 257))
+    rot_dim = head_dim if rng.random() < 0.5 else int(rng.integers(0, head_dim + 1))
+    n_heads = int(rng.integers(1, 41))
+    n_rows = int(rng.integers(1, 65))
+    base = float(rng.choice([10000.0, 500000.0, 1e6])) * float(rng.uniform(0.5, 2.0))
+    scaling = float(rng.choice([1.0, 1.0, 2.0, 4.0, 8.0])) * float(rng.uniform(0.9, 1.1))
+    pos = rng.integers(0, 1 << 20, n_rows).astype(np.int32)
+    pos[0] = 0
+    x = synth.normal(99700 + case, (n_rows, n_heads, head_dim))
+    dx = backend.buffer(x)
+    dp = backend.buffer(pos)
+    backend.rope(dx, n_rows, n_heads, head_dim, dp, base, scaling, rot_dim)
+    backend.sync()
+    got = dx.download(x.shape)
+    rot = min(rot_dim, head_dim) & ~1
+    for r in range(n_rows):
+        want = orc.rope(x[r].reshape(-1), int(pos[r]), head_dim, base, scaling, rot_dim).reshape(n_heads, head_dim)
+        err = float(np.abs(got[r] - want).max())
+        assert err <= 1e-5 * float(np.abs(x[r]).max()), (case, head_dim, rot_dim, int(pos[r]), err)
+        assert np.array_equal(got[r][:, rot:], x[r][:, rot:]), (case, r)
+    assert np.array_equal(got[0], x[0]), case   # position 0 is the identity
