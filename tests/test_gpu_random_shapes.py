@@ -4,7 +4,8 @@ decode, flash.rs:46-124 per head) with head_dim 64/128/256, GQA groups 1-8, empt
 lengths, arbitrary chunk offsets and window starts, soft-cap and sliding window on or off, f32
 and Q8_0 caches, contiguous and paged (permuted page tables with a shared prefix); and the Q8_0 matvec
 (quantized.rs:247-346) over vector counts, row counts, widths and x alignments, and RoPE
-(ops.rs:212-245) over head and rotary dimensions, bases, scalings and positions. Every case
+(ops.rs:212-245) over head and rotary dimensions, bases, scalings and positions, and KV row
+writes (cache/mod.rs:296-315) over shapes, scales and special values. Every case
 is drawn from its own fixed seed, so a failure names a reproducible
 shape. Bars: fp32 abs 1e-4 / rel 1e-3; bf16-input prefill abs 3e-2 / rel 3e-2 against the fp32
 oracle (helpers.py), and bit-identical to the per-workgroup bf16 path."""
@@ -244,3 +245,59 @@ def test_rope_random_shapes(backend, case):
         assert err <= 1e-5 * float(np.abs(x[r]).max()), (case, head_dim, rot_dim, int(pos[r]), err)
         assert np.array_equal(got[r][:, rot:], x[r][:, rot:]), (case, r)
     assert np.array_equal(got[0], x[0]), case   # position 0 is the identity
+
+
+N_KV_WRITE = 16
+
+
+@pytest.mark.parametrize("case", range(N_KV_WRITE))
+def test_kv_write_random_shapes(backend, case):
+    """KV rows written to a page pool (KvCacheQ8::quantize_into, src/cache/mod.rs:296-315, for Q8_0;
+    the f32 store's plain copy) through the host and the device entry points, over seeded KV head
+    counts, head dims, row scales from 1e-12 to 1e7 (f16 block scales that flush to zero, go
+    subnormal or overflow to inf), NaN and +-inf entries and exact .5 multiples of the scale,
+    exported in the reference's row format and compared byte for byte with the oracle; then
+    imported into other rows and exported again unchanged."""
+    rng = np.random.default_rng(99400 + case)
+    dtype = "q8" if case % 4 else "f32"
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    d = int(rng.choice([64, 128, 256]))
+    kv_dim = hkv * d
+    pages = int(rng.integers(4, 41))
+    n = int(rng.integers(1, pages * 16 // 2 + 1))
+    rows = rng.permutation(pages * 16)[: 2 * n].astype(np.int64)
+    src, dst = rows[:n], rows[n:]
+    x = (rng.standard_normal((2, n, kv_dim)) * 10.0 ** rng.uniform(-12, 7, (2, n, 1))).astype(np.float32)
+    for t in range(2):
+        for r in rng.choice(n, size=min(n, 6), replace=False):
+            kind = int(rng.integers(0, 5))
+            c = int(rng.integers(0, kv_dim))
+            if kind == 0:
+                x[t, r, c] = np.nan
+            elif kind == 1:
+                x[t, r, c] = np.inf if rng.random() < 0.5 else -np.inf
+            elif kind == 2:
+                x[t, r, (c // 32) * 32:(c // 32) * 32 + 32] = 0.0
+            elif kind == 3:     # quants that land on .5 before rounding: 127 * (k + 0.5) / 127
+                blk = slice((c // 32) * 32, (c // 32) * 32 + 32)
+                x[t, r, blk] = (rng.integers(-127, 127, 32) + 0.5).astype(np.float32)
+                x[t, r, (c // 32) * 32] = 127.0
+            else:
+                x[t, r, c] = -x[t, r, c] * 1e3
+    k, v = x[0], x[1]
+    pool = backend.create_page_pool(pages, hkv, d, dtype)
+    half = n // 2
+    pool.write_rows(src[:half], k[:half], v[:half])
+    if n > half:
+        pool.write_rows_device(backend.buffer(src[half:]), backend.buffer(k[half:]), backend.buffer(v[half:]), n - half)
+    kb, vb = pool.export_rows(src)
+    if dtype == "q8":
+        assert np.array_equal(kb, orc.q8_quantize_rows(k)), case
+        assert np.array_equal(vb, orc.q8_quantize_rows(v)), case
+    else:
+        assert np.array_equal(kb.view(np.uint32).reshape(n, kv_dim), k.view(np.uint32)), case
+        assert np.array_equal(vb.view(np.uint32).reshape(n, kv_dim), v.view(np.uint32)), case
+    pool.import_rows(dst, kb, vb)
+    k2, v2 = pool.export_rows(dst)
+    assert np.array_equal(k2, kb) and np.array_equal(v2, vb), case
+    pool.destroy()
