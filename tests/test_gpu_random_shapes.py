@@ -5,7 +5,8 @@ lengths, arbitrary chunk offsets and window starts, soft-cap and sliding window 
 and Q8_0 caches, contiguous and paged (permuted page tables with a shared prefix); and the Q8_0 matvec
 (quantized.rs:247-346) over vector counts, row counts, widths and x alignments, and RoPE
 (ops.rs:212-245) over head and rotary dimensions, bases, scalings and positions, and KV row
-writes (cache/mod.rs:296-315) over shapes, scales and special values. Every case
+writes (cache/mod.rs:296-315) over shapes, scales and special values, and the host-pointer
+attention entry points (backend/gpu.rs:266-397, :860-992). Every case
 is drawn from its own fixed seed, so a failure names a reproducible
 shape. Bars: fp32 abs 1e-4 / rel 1e-3; bf16-input prefill abs 3e-2 / rel 3e-2 against the fp32
 oracle (helpers.py), and bit-identical to the per-workgroup bf16 path."""
@@ -301,3 +302,42 @@ def test_kv_write_random_shapes(backend, case):
     k2, v2 = pool.export_rows(dst)
     assert np.array_equal(k2, kb) and np.array_equal(v2, vb), case
     pool.destroy()
+
+
+N_HOST_ATTN = 16
+
+
+@pytest.mark.parametrize("case", range(N_HOST_ATTN))
+def test_host_attention_random_shapes(backend, case):
+    """The host-pointer entry points over seeded shapes: GpuBackend::attention (host q and K/V,
+    src/backend/gpu.rs:266-397) and attention_resident (host q over a device cache, a sequence
+    slot, a layer and a window, gpu.rs:860-992), against the oracle's batched decode of the
+    same rows at the fp32 bar."""
+    rng = np.random.default_rng(99300 + case)
+    d = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    H = hkv * int(rng.choice([1, 2, 3, 4, 8]))
+    cap = None if rng.random() < 0.5 else float(rng.uniform(5.0, 60.0))
+    scale = float(1.0 / np.sqrt(d)) * float(rng.uniform(0.5, 2.0))
+    kv_dim = hkv * d
+    # host K/V
+    seq_len = int(rng.integers(1, 2501))
+    k = synth.normal(99310 + case, (1, seq_len, kv_dim))
+    v = synth.normal(99320 + case, (1, seq_len, kv_dim))
+    q = synth.normal(99330 + case, (1, H * d))
+    want = orc.decode_batch(q, [orc.kv_cache(k, v)], 0, [0], [seq_len], H, hkv, d, scale, cap)
+    got = backend.attention(q[0], k[0], v[0], H, hkv, d, seq_len, scale, cap)
+    assert_close(got.reshape(1, -1), want, what=f"case {case} attention d {d} H {H}/{hkv} len {seq_len}")
+    # resident cache
+    dtype = str(rng.choice(["f32", "q8"]))
+    n_seqs = int(rng.integers(1, 4))
+    max_seq = int(rng.integers(1, 2001))
+    c = Contig(backend, dtype, n_seqs, 2, max_seq, hkv, d, seed=99340 + case)
+    seq = int(rng.integers(0, n_seqs))
+    layer = int(rng.integers(0, 2))
+    start = int(rng.integers(0, max_seq))
+    attend = int(rng.integers(1, max_seq - start + 1))
+    want = orc.decode_batch(q, [c.stores[seq]], layer, [start], [attend], H, hkv, d, scale, cap)
+    got = backend.attention_resident(q[0], c.cache, layer, start, attend, H, hkv, d, scale, cap, seq=seq)
+    assert_close(got.reshape(1, -1), want,
+                 what=f"case {case} resident {dtype} d {d} H {H}/{hkv} seq {seq} layer {layer} [{start}, +{attend})")
