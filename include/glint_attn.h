@@ -130,7 +130,10 @@ int64_t gla_kv_row_id(const gla_kv *kv, int seq, int layer, int pos);
  * KvStore::write analogue (src/cache/mod.rs:166-177, :374-388,
  * src/cache/paged.rs:467-490). Q8_0 storage quantises on write with the
  * rules of KvCacheQ8::quantize_into (src/cache/mod.rs:296-315), bit-exactly.
- * Device pointers; asynchronous. rows: int64[n_rows]; k, v: [n_rows][kv_dim]. */
+ * Device pointers; asynchronous. rows: int64[n_rows]; k, v: [n_rows][kv_dim].
+ * The rows are written in parallel: ids repeated within one call leave one
+ * of their rows (which one is unspecified), and ids outside the storage are
+ * skipped on the device. */
 int gla_kv_write_rows(gla_ctx *ctx, gla_kv *kv, const int64_t *rows_dev, const float *k_dev,
                       const float *v_dev, int n_rows);
 /* The same with host pointers; returns when the rows are written. */
