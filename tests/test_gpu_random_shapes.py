@@ -341,3 +341,36 @@ def test_host_attention_random_shapes(backend, case):
     got = backend.attention_resident(q[0], c.cache, layer, start, attend, H, hkv, d, scale, cap, seq=seq)
     assert_close(got.reshape(1, -1), want,
                  what=f"case {case} resident {dtype} d {d} H {H}/{hkv} seq {seq} layer {layer} [{start}, +{attend})")
+
+
+N_ODD_GROUPS = 12
+
+
+@pytest.mark.parametrize("case", range(N_ODD_GROUPS))
+def test_decode_odd_groups_random(backend, case):
+    """Decode with GQA groups that do not fill the kernels' 4-head wave groups (3, 5, 6, 7) or
+    span several of them (12, 16), contiguous and paged, f32 and Q8_0, against the oracle."""
+    rng = np.random.default_rng(99200 + case)
+    d = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2, 3, 4]))
+    group = int(rng.choice([3, 5, 6, 7, 12, 16]))
+    H = hkv * group
+    B = int(rng.integers(1, 7))
+    ctx = np.asarray(rng.integers(1, 2501, B), np.int32)
+    cap = None if rng.random() < 0.5 else float(rng.uniform(5.0, 60.0))
+    dtype = str(rng.choice(["f32", "q8"]))
+    scale = float(1.0 / np.sqrt(d)) * float(rng.uniform(0.5, 2.0))
+    q = synth.normal(99210 + case, (B, H, d))
+    if case % 2:
+        pb = synth.paged_batch(99220 + case, ctx, prefix_tokens=int(rng.choice([0, 32])))
+        p = Pool(backend, dtype, pb, hkv, d, seed=99230 + case)
+        w = synth.windowed(pb, None)
+        want = orc.decode_batch(q.reshape(B, H * d), p.stores, 0, w.kv_start, w.kv_len, H, hkv, d, scale, cap)
+        got = run_decode(backend, p.pool, q, w.kv_start, w.kv_len, H, scale, cap, table=pb.table)
+    else:
+        c = Contig(backend, dtype, B, 1, int(ctx.max()), hkv, d, seed=99240 + case)
+        starts = np.asarray([int(rng.integers(0, t)) for t in ctx], np.int32)
+        lens = ctx - starts
+        want = orc.decode_batch(q.reshape(B, H * d), c.stores, 0, starts, lens, H, hkv, d, scale, cap)
+        got = run_decode(backend, c.cache, q, starts, lens, H, scale, cap)
+    assert_close(got, want.reshape(B, H, d), what=f"case {case} d {d} H {H}/{hkv} {dtype} B {B}")
