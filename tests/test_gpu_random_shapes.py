@@ -374,3 +374,39 @@ def test_decode_odd_groups_random(backend, case):
         want = orc.decode_batch(q.reshape(B, H * d), c.stores, 0, starts, lens, H, hkv, d, scale, cap)
         got = run_decode(backend, c.cache, q, starts, lens, H, scale, cap)
     assert_close(got, want.reshape(B, H, d), what=f"case {case} d {d} H {H}/{hkv} {dtype} B {B}")
+
+
+N_PREFILL_ODD = 10
+
+
+@pytest.mark.parametrize("case", range(N_PREFILL_ODD))
+def test_prefill_odd_groups_random(backend, monkeypatch, case):
+    """Prefill with GQA groups 5, 6, 7, 12 and 16 (the workgroup's heads-per-KV-head split
+    part-filled or repeated), f32 and bf16-input, against the oracle; bf16 also bit-identical
+    to the per-workgroup path."""
+    rng = np.random.default_rng(99100 + case)
+    d = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2]))
+    H = hkv * int(rng.choice([5, 6, 7, 12, 16]))
+    lens = [int(x) for x in rng.integers(1, 200, int(rng.integers(1, 3)))]
+    offs = [int(x) for x in rng.integers(0, 100, len(lens))]
+    window = None if rng.random() < 0.5 else int(rng.integers(1, 200))
+    cap = None if rng.random() < 0.5 else float(rng.uniform(5.0, 60.0))
+    dtype = str(rng.choice(["f32", "q8"]))
+    precision = "bf16" if case % 2 else "f32"
+    scale = float(1.0 / np.sqrt(d))
+    c = Contig(backend, dtype, len(lens), 1, max(o + n for o, n in zip(offs, lens)), hkv, d, seed=99110 + case)
+    q = synth.normal(99120 + case, (sum(lens), H, d))
+    q_start = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    monkeypatch.delenv("GLA_BF16_UNSTAGED", raising=False)
+    got = run_prefill(backend, c.cache, q, q_start, offs, H, scale, cap, window, precision=precision)
+    tol = (BF16_ABS_TOL, BF16_REL_TOL) if precision == "bf16" else ()
+    for b, n in enumerate(lens):
+        rows = slice(q_start[b], q_start[b + 1])
+        want = orc.prefill(q[rows].reshape(n, H * d), c.stores[b], 0, offs[b], H, hkv, d, scale, cap,
+                           window).reshape(n, H, d)
+        assert_close(got[rows], want, *tol, what=f"case {case} d {d} H {H}/{hkv} {dtype} {precision} seq {b}")
+    if precision == "bf16":
+        monkeypatch.setenv("GLA_BF16_UNSTAGED", "1")
+        unstaged = run_prefill(backend, c.cache, q, q_start, offs, H, scale, cap, window, precision="bf16")
+        assert np.array_equal(got.view(np.uint32), unstaged.view(np.uint32)), case
