@@ -299,3 +299,22 @@ def test_cfg5_gemma2_windowed_and_global(backend):
         want = _oracle_decode(p.stores, q, ws, kl, H, Hkv, d, 1 / 16.0, 50.0)
         got = run_decode(backend, p.pool, q, ws, kl, H, 1 / 16.0, 50.0, table=pb.table)
         assert_close(got, want, what=f"cfg5 layer {layer}")
+
+
+def test_q8_host_lengths_beyond_the_row_list(backend, monkeypatch):
+    """Host lengths whose workgroups overflow the kernel-argument row list (1,536 entries: here
+    2-page chunks, 8 pages per workgroup, 120 sequences of ~2,000 positions): the launch falls
+    back to the (unit, workgroup, sequence) grid sized from the host lengths. Same bits as
+    without host lengths, and the oracle's values."""
+    monkeypatch.setenv("GLA_Q8_CHUNK_PAGES", "2")
+    H, Hkv, d = 8, 2, 64
+    ctx = synth.uniform_int(831, 1500, 2500, 120)
+    pb = synth.paged_batch(832, ctx, prefix_tokens=32)
+    p = Pool(backend, "q8", pb, Hkv, d, seed=833)
+    q = synth.normal(834, (len(ctx), H, d))
+    assert sum(-(-int(n) // 128) for n in ctx) > 1536
+    want = _oracle_decode(p.stores, q, pb.kv_start, pb.kv_len, H, Hkv, d, 0.125)
+    a = run_decode(backend, p.pool, q, pb.kv_start, pb.kv_len, H, 0.125, table=pb.table, host_lengths=True)
+    b = run_decode(backend, p.pool, q, pb.kv_start, pb.kv_len, H, 0.125, table=pb.table, host_lengths=False)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert_close(a, want, what="q8 host lengths past the row list")
