@@ -496,128 +496,6 @@ Status PagedKvCache::import_raw(const std::vector<std::vector<uint8_t>> &k_layer
     return {};
 }
 
-// ---- PrefixCache -----------------------------------------------------------------------
-
-std::vector<uint64_t> page_chain(const uint32_t *tokens, size_t n) {
-    constexpr uint64_t kOffset = 0xcbf29ce484222325ull;  // FNV-1a 64-bit parameters
-    constexpr uint64_t kPrime = 0x100000001b3ull;
-    std::vector<uint64_t> out;
-    out.reserve(n / PAGE_SIZE);
-    uint64_t prev = 0;
-    for (size_t p = 0; p + PAGE_SIZE <= n; p += PAGE_SIZE) {
-        uint64_t h = kOffset;
-        for (int i = 0; i < 8; i++) h = (h ^ ((prev >> (8 * i)) & 0xff)) * kPrime;
-        for (size_t t = p; t < p + PAGE_SIZE; t++)
-            for (int i = 0; i < 4; i++) h = (h ^ ((tokens[t] >> (8 * i)) & 0xff)) * kPrime;
-        out.push_back(h);
-        prev = h;
-    }
-    return out;
-}
-
-PrefixCache::PrefixCache(PrefixCacheConfig config) : config_(config) {}
-
-std::optional<PagedKvCache> PrefixCache::lookup(const std::vector<uint32_t> &prompt, const char *lora) {
-    const size_t usable_pages = prompt.empty() ? 0 : (prompt.size() - 1) / PAGE_SIZE;
-    if (usable_pages < MIN_SHARED_PAGES || entries_.empty()) {
-        stats_.misses += 1;
-        return std::nullopt;
-    }
-    const std::vector<uint64_t> chain = page_chain(prompt.data(), usable_pages * PAGE_SIZE);
-    size_t best = entries_.size(), best_pages = 0;
-    for (size_t i = 0; i < entries_.size(); i++) {
-        const Entry &e = entries_[i];
-        if (!same_lora(e.lora, lora)) continue;
-        size_t shared = 0;
-        while (shared < e.page_hashes.size() && shared < chain.size() && e.page_hashes[shared] == chain[shared])
-            shared++;
-        if (shared >= MIN_SHARED_PAGES && (best == entries_.size() || shared > best_pages)) {
-            best = i;
-            best_pages = shared;
-        }
-    }
-    if (best == entries_.size()) {
-        stats_.misses += 1;
-        return std::nullopt;
-    }
-    const size_t upto = best_pages * PAGE_SIZE;
-    // the hashes index; the tokens decide (a collision is a miss, never wrong K/V)
-    if (!std::equal(prompt.begin(), prompt.begin() + (ptrdiff_t)upto, entries_[best].tokens.begin())) {
-        stats_.misses += 1;
-        return std::nullopt;
-    }
-    clock_ += 1;
-    entries_[best].last_used = clock_;
-    stats_.hits += 1;
-    stats_.tokens_reused += upto;
-    return entries_[best].cache.fork_from(upto);
-}
-
-void PrefixCache::insert(const std::vector<uint32_t> &prompt, const PagedKvCache &cache, const char *lora) {
-    const size_t pages = prompt.size() / PAGE_SIZE;
-    const size_t upto = pages * PAGE_SIZE;
-    if (pages < MIN_SHARED_PAGES || upto > cache.len()) return;
-    const std::vector<uint32_t> tokens(prompt.begin(), prompt.begin() + (ptrdiff_t)upto);
-    clock_ += 1;
-    const uint64_t stamp = clock_;
-    for (Entry &e : entries_)
-        if (same_lora(e.lora, lora) && e.tokens == tokens) {  // already held: a touch
-            e.last_used = stamp;
-            return;
-        }
-    // shorter prefixes of this one hold pages this fork holds too: drop them
-    for (size_t i = 0; i < entries_.size();) {
-        const Entry &e = entries_[i];
-        const bool superseded = same_lora(e.lora, lora) && e.tokens.size() < tokens.size() &&
-                                std::equal(e.tokens.begin(), e.tokens.end(), tokens.begin());
-        if (superseded) {
-            if (i + 1 != entries_.size()) std::swap(entries_[i], entries_.back());
-            entries_.pop_back();
-        } else {
-            i++;
-        }
-    }
-    PagedKvCache fork = cache.fork_from(upto);
-    const size_t held = fork.allocated_pages();
-    entries_.push_back(Entry{tokens, page_chain(tokens.data(), tokens.size()),
-                             lora ? std::optional<std::string>(lora) : std::nullopt, std::move(fork), held, stamp});
-    enforce_budget();
-}
-
-bool PrefixCache::evict_lru() {
-    if (entries_.empty()) return false;
-    size_t idx = 0;
-    for (size_t i = 1; i < entries_.size(); i++)
-        if (entries_[i].last_used < entries_[idx].last_used) idx = i;
-    if (idx + 1 != entries_.size()) std::swap(entries_[idx], entries_.back());
-    entries_.pop_back();  // releases the pages no other holder shares
-    stats_.evictions += 1;
-    return true;
-}
-
-void PrefixCache::clear() {
-    stats_.evictions += entries_.size();
-    entries_.clear();
-}
-
-size_t PrefixCache::pages() const {
-    size_t n = 0;
-    for (const Entry &e : entries_) n += e.pages;
-    return n;
-}
-
-PrefixCacheStats PrefixCache::stats() const {
-    PrefixCacheStats s = stats_;
-    s.entries = entries_.size();
-    s.pages = pages();
-    return s;
-}
-
-void PrefixCache::enforce_budget() {
-    while (entries_.size() > config_.max_entries || pages() > config_.max_pages)
-        if (!evict_lru()) return;
-}
-
 // ---- GpuKvCache ------------------------------------------------------------------------
 
 class GpuKvStorage {

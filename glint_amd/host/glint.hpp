@@ -7,7 +7,6 @@
 //   KvStore                       src/cache/mod.rs:24-109
 //   PagePool / PagedKvCache       src/cache/paged.rs:55-598
 //   GpuKvBuffer / GpuKvCache      src/backend/gpu.rs:1005-1104, src/cache/mod.rs:430-578
-//   PrefixCache                   src/cache/prefix.rs:53-337
 //   GpuBackend::attention{,_resident}, create_kv_cache
 //                                 src/backend/gpu.rs:41-56, :266-397, :860-992, :1058-1104
 //   batched decode / prefill attention steps
@@ -359,77 +358,6 @@ class PagedKvCache final : public KvStore {
     std::vector<std::vector<int32_t>> table_;  // table_[layer][page] = device page id
     size_t len_ = 0;
 };
-
-// ---- PrefixCache -----------------------------------------------------------------
-
-// Registry of reusable prompt prefixes over device pages (src/cache/prefix.rs:
-// 53-337): retains a page-sharing fork of completed prefills and hands the
-// longest cached whole-page prefix of a new prompt to its sequence. Keyed by
-// a chained per-page hash, verified against the tokens before a fork is
-// handed out; bounded by entries and by pages held, evicting the least
-// recently used entry.
-constexpr size_t MIN_SHARED_PAGES = 1;
-
-struct PrefixCacheStats {
-    uint64_t hits = 0;           // lookups that returned a fork
-    uint64_t misses = 0;         // lookups that found nothing to reuse
-    uint64_t evictions = 0;      // entries dropped (budget or caller)
-    uint64_t tokens_reused = 0;  // prompt positions served from cached pages
-    size_t entries = 0;
-    size_t pages = 0;            // upper bound, see PrefixCache::pages
-    bool operator==(const PrefixCacheStats &o) const {
-        return hits == o.hits && misses == o.misses && evictions == o.evictions &&
-               tokens_reused == o.tokens_reused && entries == o.entries && pages == o.pages;
-    }
-};
-
-struct PrefixCacheConfig {
-    size_t max_entries = 16;
-    size_t max_pages = 512;
-};
-
-class PrefixCache {
-  public:
-    explicit PrefixCache(PrefixCacheConfig config = PrefixCacheConfig());
-    // Longest cached prefix of `prompt` (whole pages, at least one token left
-    // to prefill) under adapter `lora` (nullptr: base weights), as a fork
-    // whose len() is the number of prompt positions already present.
-    std::optional<PagedKvCache> lookup(const std::vector<uint32_t> &prompt, const char *lora = nullptr);
-    // Retain the complete pages of `prompt` that `cache` has computed.
-    void insert(const std::vector<uint32_t> &prompt, const PagedKvCache &cache, const char *lora = nullptr);
-    // Drop the least recently used entry; false when there is none.
-    bool evict_lru();
-    void clear();
-    size_t len() const { return entries_.size(); }
-    bool is_empty() const { return entries_.empty(); }
-    // Pages retained, summed per entry (an upper bound on what the registry
-    // keeps from the pool: shared ancestors count once per entry).
-    size_t pages() const;
-    PrefixCacheStats stats() const;
-
-  private:
-    struct Entry {
-        std::vector<uint32_t> tokens;  // exactly the cached prefix, whole pages
-        std::vector<uint64_t> page_hashes;
-        std::optional<std::string> lora;
-        PagedKvCache cache;  // fork of the producing sequence, len() == tokens.size()
-        size_t pages;
-        uint64_t last_used;
-    };
-    static bool same_lora(const std::optional<std::string> &a, const char *b) {
-        return b ? (a && *a == b) : !a;
-    }
-    void enforce_budget();
-    std::vector<Entry> entries_;
-    PrefixCacheConfig config_;
-    uint64_t clock_ = 0;
-    PrefixCacheStats stats_;
-};
-
-// Chained hash of every complete page of tokens[0, n): h[p] = FNV-1a 64 over
-// the little-endian bytes of h[p-1] (0 before page 0) and of page p's 16
-// token ids, so equal hashes at page p mean the prefixes agree up to p.
-std::vector<uint64_t> page_chain(const uint32_t *tokens, size_t n);
 
 // ---- GpuKvCache ------------------------------------------------------------------
 

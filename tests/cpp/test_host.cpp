@@ -534,7 +534,7 @@ struct Rng {
     }
 };
 
-// ---- PrefixCache (src/cache/prefix.rs:338-786) ---------------------------------------------
+// ---- page-sharing fork over a device pool -------------------------------------------------
 
 // A cache holding tokens.size() positions, rows derived from the token ids.
 PagedKvCache filled(const PagePool &shared, const std::vector<uint32_t> &tokens) {
@@ -565,339 +565,36 @@ std::vector<uint32_t> cat(std::vector<uint32_t> a, const std::vector<uint32_t> &
     return a;
 }
 
-PrefixCache registry() { return PrefixCache(PrefixCacheConfig{4, 64}); }
-
-TEST(test_lookup_returns_longest_page_aligned_prefix) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto a = cat(prompt(40, 0), {1, 1, 1});
-    auto b = cat(prompt(40, 0), {2, 2, 2});
-    pc.insert(a, filled(shared, a));
-    auto fork = pc.lookup(b);
-    CHECK(fork.has_value());
-    CHECK_EQ(fork->len(), 32u);
-    CHECK_EQ(pc.stats().hits, 1u);
-    CHECK_EQ(pc.stats().tokens_reused, 32u);
-}
-
-TEST(test_lookup_shares_whole_pages_only) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto a = cat(prompt(20, 0), {3, 3});
-    auto b = cat(prompt(20, 0), {4, 4});
-    pc.insert(a, filled(shared, a));
-    auto fork = pc.lookup(b);
-    CHECK(fork.has_value());
-    CHECK_EQ(fork->len(), PAGE_SIZE);
-    CHECK_EQ(fork->pages_per_layer(), 1u);
-}
-
-TEST(test_lookup_always_leaves_a_suffix_to_prefill) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto tokens = prompt(32, 0);
-    pc.insert(tokens, filled(shared, tokens));
-    auto fork = pc.lookup(tokens);
-    CHECK(fork.has_value());
-    CHECK_EQ(fork->len(), 16u);
-}
-
-TEST(test_lookup_below_one_page_is_a_miss) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto tokens = prompt(32, 0);
-    pc.insert(tokens, filled(shared, tokens));
-    CHECK(!pc.lookup(std::vector<uint32_t>(tokens.begin(), tokens.begin() + 16)).has_value());
-    CHECK(!pc.lookup({1, 2, 3}).has_value());
-    CHECK_EQ(pc.stats().misses, 2u);
-}
-
-TEST(test_lookup_on_an_empty_registry_is_a_miss) {
-    PrefixCache pc = registry();
-    CHECK(!pc.lookup(prompt(64, 0)).has_value());
-    PrefixCacheStats want;
-    want.misses = 1;
-    CHECK(pc.stats() == want);
-}
-
-TEST(test_lookup_rejects_a_different_prompt) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto a = prompt(48, 0), b = prompt(48, 1);
-    pc.insert(a, filled(shared, a));
-    CHECK(!pc.lookup(b).has_value());
-}
-
-TEST(test_entries_are_keyed_by_lora_adapter) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto tokens = prompt(48, 0);
-    pc.insert(tokens, filled(shared, tokens), "adapter-a");
-    CHECK(!pc.lookup(tokens).has_value());
-    CHECK(!pc.lookup(tokens, "adapter-b").has_value());
-    CHECK(pc.lookup(tokens, "adapter-a").has_value());
-}
-
-TEST(test_lookup_picks_the_longest_match) {
-    auto shared = pool(128);
-    PrefixCache pc = registry();
-    auto longp = prompt(80, 0);
-    auto short_divergent = cat(std::vector<uint32_t>(longp.begin(), longp.begin() + 32), prompt(32, 5));
-    pc.insert(short_divergent, filled(shared, short_divergent));
-    pc.insert(longp, filled(shared, longp));
-    auto fork = pc.lookup(longp);
-    CHECK(fork.has_value());
-    CHECK_EQ(fork->len(), 64u);
-}
-
-TEST(test_insert_never_caches_past_the_prompt) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto tokens = prompt(20, 0);
-    PagedKvCache cache = filled(shared, tokens);
-    cache.reserve(50).expect("pool has room");
-    std::vector<float> k(KV_DIM, 0.5f), v(KV_DIM, 0.25f);
-    for (size_t i = 0; i < 30; i++) {
-        for (size_t layer = 0; layer < N_LAYERS; layer++) cache.write(layer, 20 + i, k.data(), v.data());
-        cache.advance();
-    }
-    pc.insert(tokens, cache);
-    CHECK_EQ(pc.len(), 1u);
-    auto fork = pc.lookup(cat(tokens, {1, 2}));
-    CHECK(fork.has_value());
-    CHECK_EQ(fork->len(), PAGE_SIZE);
-}
-
-TEST(test_insert_below_one_page_is_ignored) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto tokens = prompt(15, 0);
-    pc.insert(tokens, filled(shared, tokens));
-    CHECK(pc.is_empty());
-}
-
-TEST(test_insert_of_a_known_prefix_is_a_touch) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto tokens = prompt(32, 0);
-    pc.insert(tokens, filled(shared, tokens));
-    const size_t pages_after_first = pc.pages();
-    pc.insert(tokens, filled(shared, tokens));
-    CHECK_EQ(pc.len(), 1u);
-    CHECK_EQ(pc.pages(), pages_after_first);
-}
-
-TEST(test_insert_supersedes_a_shorter_prefix) {
-    auto shared = pool(128);
-    PrefixCache pc = registry();
-    auto longp = prompt(64, 0);
-    std::vector<uint32_t> half(longp.begin(), longp.begin() + 32);
-    pc.insert(half, filled(shared, half));
-    CHECK_EQ(pc.len(), 1u);
-    pc.insert(longp, filled(shared, longp));
-    CHECK_EQ(pc.len(), 1u);
-    auto fork = pc.lookup(longp);
-    CHECK(fork.has_value());
-    CHECK_EQ(fork->len(), 48u);
-}
-
-TEST(test_diverging_prompts_keep_separate_entries) {
-    auto shared = pool(128);
-    PrefixCache pc = registry();
-    auto a = prompt(48, 0), b = prompt(48, 1);
-    pc.insert(a, filled(shared, a));
-    pc.insert(b, filled(shared, b));
-    CHECK_EQ(pc.len(), 2u);
-}
-
-TEST(test_evict_lru_drops_the_least_recently_used_entry) {
-    auto shared = pool(128);
-    PrefixCache pc = registry();
-    auto a = prompt(32, 0), b = prompt(32, 1);
-    pc.insert(a, filled(shared, a));
-    pc.insert(b, filled(shared, b));
-    CHECK(pc.lookup(a).has_value());
-    CHECK(pc.evict_lru());
-    CHECK_EQ(pc.len(), 1u);
-    CHECK(pc.lookup(a).has_value());
-    CHECK(!pc.lookup(b).has_value());
-    CHECK_EQ(pc.stats().evictions, 1u);
-}
-
-TEST(test_evict_lru_on_an_empty_registry_reports_nothing_to_do) {
-    PrefixCache pc = registry();
-    CHECK(!pc.evict_lru());
-}
-
-TEST(test_eviction_returns_pages_to_the_pool) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto tokens = prompt(32, 0);
-    {
-        PagedKvCache cache = filled(shared, tokens);
-        pc.insert(tokens, cache);
-    }
-    CHECK_EQ(shared.live_pages(), 2 * N_LAYERS);
-    CHECK(pc.evict_lru());
-    CHECK_EQ(shared.live_pages(), 0u);
-}
-
-TEST(test_eviction_keeps_pages_a_live_sequence_still_shares) {
-    auto shared = pool(64);
-    PrefixCache pc = registry();
-    auto tokens = prompt(32, 0);
-    auto live = std::make_unique<PagedKvCache>(filled(shared, tokens));
-    pc.insert(tokens, *live);
-    const size_t held = shared.live_pages();
-    CHECK(pc.evict_lru());
-    CHECK_EQ(shared.live_pages(), held);
-    live.reset();
-    CHECK_EQ(shared.live_pages(), 0u);
-}
-
-TEST(test_entry_budget_evicts_the_oldest) {
+// A sequence forked from another's whole-page prefix (the pages an engine-side
+// prefix registry hands out, src/cache/paged.rs:433-444) and then given its
+// own suffix decodes bit for bit like a sequence that computed the whole
+// prompt itself (device). The suffix's first write copies the shared partial
+// page on write.
+DEVICE_TEST(test_fork_decode_equals_cold_sequence) {
     auto shared = pool(256);
-    PrefixCache pc(PrefixCacheConfig{2, 1024});
-    std::vector<std::vector<uint32_t>> prompts;
-    for (uint32_t i = 0; i < 3; i++) prompts.push_back(prompt(32, i));
-    for (auto &p : prompts) pc.insert(p, filled(shared, p));
-    CHECK_EQ(pc.len(), 2u);
-    CHECK(!pc.lookup(prompts[0]).has_value());
-    CHECK(pc.lookup(prompts[2]).has_value());
-    CHECK_EQ(pc.stats().evictions, 1u);
-}
-
-TEST(test_page_budget_evicts_until_it_fits) {
-    auto shared = pool(256);
-    PrefixCache pc(PrefixCacheConfig{16, 2 * N_LAYERS});
-    auto a = prompt(32, 0), b = prompt(32, 1);
-    pc.insert(a, filled(shared, a));
-    CHECK_EQ(pc.len(), 1u);
-    pc.insert(b, filled(shared, b));
-    CHECK_EQ(pc.len(), 1u);
-    CHECK(pc.pages() <= 2 * N_LAYERS);
-}
-
-TEST(test_clear_releases_everything) {
-    auto shared = pool(128);
-    PrefixCache pc = registry();
-    auto tokens = prompt(32, 0);
-    pc.insert(tokens, filled(shared, tokens));
-    pc.clear();
-    CHECK(pc.is_empty());
-    CHECK_EQ(shared.live_pages(), 0u);
-    CHECK_EQ(pc.stats().evictions, 1u);
-}
-
-TEST(test_fork_carries_the_cached_rows) {
-    auto shared = pool(128);
-    PrefixCache pc = registry();
-    auto tokens = prompt(48, 0);
-    PagedKvCache source = filled(shared, tokens);
-    pc.insert(tokens, source);
-    auto fork = pc.lookup(tokens);
-    CHECK(fork.has_value());
-    for (size_t layer = 0; layer < N_LAYERS; layer++)
-        for (size_t pos = 0; pos < fork->len(); pos++) {
-            CHECK(rows_equal(fork->k_at(layer, pos), source.k_at(layer, pos)));
-            CHECK(rows_equal(fork->v_at(layer, pos), source.v_at(layer, pos)));
-        }
-}
-
-TEST(test_two_forks_diverge_without_corrupting_the_entry) {
-    auto shared = pool(128);
-    PrefixCache pc = registry();
-    auto base = prompt(32, 0);
-    pc.insert(base, filled(shared, base));
-    auto fa = pc.lookup(cat(base, {1, 1}));
-    auto fb = pc.lookup(cat(base, {2, 2}));
-    CHECK(fa.has_value() && fb.has_value());
-    const size_t start = fa->len();
-    for (auto pr : {std::make_pair(&*fa, 11.0f), std::make_pair(&*fb, 22.0f)}) {
-        pr.first->reserve(start + 2).expect("pool has room");
-        std::vector<float> row_(KV_DIM, pr.second);
-        for (size_t pos = start; pos < start + 2; pos++) {
-            for (size_t layer = 0; layer < N_LAYERS; layer++) pr.first->write(layer, pos, row_.data(), row_.data());
-            pr.first->advance();
-        }
-    }
-    CHECK(rows_equal(fa->k_at(0, start), std::vector<float>(KV_DIM, 11.0f)));
-    CHECK(rows_equal(fb->k_at(0, start), std::vector<float>(KV_DIM, 22.0f)));
-    for (size_t pos = 0; pos < start; pos++) CHECK(rows_equal(fa->k_at(0, pos), fb->k_at(0, pos)));
-}
-
-TEST(test_page_chain_is_a_prefix_key) {
-    auto a = prompt(64, 0);
-    auto b = cat(std::vector<uint32_t>(a.begin(), a.begin() + 32), prompt(32, 3));
-    auto ha = page_chain(a.data(), a.size()), hb = page_chain(b.data(), b.size());
-    CHECK_EQ(ha.size(), 4u);
-    CHECK(ha[0] == hb[0] && ha[1] == hb[1]);
-    CHECK(ha[2] != hb[2]);
-}
-
-TEST(test_page_chain_ignores_a_partial_tail) {
-    auto t = prompt(20, 0);
-    CHECK_EQ(page_chain(t.data(), 20).size(), 1u);
-    CHECK(page_chain(t.data(), 16) == page_chain(t.data(), 20));
-}
-
-// FNV-1a 64 known answers (the published test vectors of the hash the page
-// chain applies): the empty input hashes to the offset basis, and "a" to
-// 0xaf63dc4c8601ec8c. A page chain's first value is FNV-1a over 8 zero bytes
-// then the page's token bytes, restated here byte by byte.
-HOST_TEST(test_page_chain_matches_fnv1a_restated) {
-    auto fnv = [](const std::vector<uint8_t> &bytes) {
-        uint64_t h = 0xcbf29ce484222325ull;
-        for (uint8_t x : bytes) h = (h ^ x) * 0x100000001b3ull;
-        return h;
-    };
-    CHECK(fnv({}) == 0xcbf29ce484222325ull);
-    CHECK(fnv({'a'}) == 0xaf63dc4c8601ec8cull);
-    auto t = prompt(32, 9);
-    std::vector<uint8_t> bytes(8, 0);
-    for (size_t i = 0; i < 16; i++)
-        for (int s = 0; s < 4; s++) bytes.push_back((uint8_t)(t[i] >> (8 * s)));
-    const uint64_t h0 = fnv(bytes);
-    std::vector<uint8_t> bytes1;
-    for (int s = 0; s < 8; s++) bytes1.push_back((uint8_t)(h0 >> (8 * s)));
-    for (size_t i = 16; i < 32; i++)
-        for (int s = 0; s < 4; s++) bytes1.push_back((uint8_t)(t[i] >> (8 * s)));
-    auto chain = page_chain(t.data(), t.size());
-    CHECK(chain.size() == 2 && chain[0] == h0 && chain[1] == fnv(bytes1));
-}
-
-// The decode over a prefix-cache fork plus its own suffix equals the decode
-// over a sequence that computed the whole prompt (device).
-DEVICE_TEST(test_prefix_fork_decode_equals_cold_sequence) {
-    auto shared = pool(256);
-    PrefixCache pc = registry();
     auto base = prompt(70, 0);
-    pc.insert(base, filled(shared, base));
+    PagedKvCache parent = filled(shared, base);
+    PagedKvCache fork = parent.fork_from(64);
+    CHECK_EQ(fork.len(), 64u);
     auto full = cat(base, prompt(25, 3));
-    auto fork = pc.lookup(full);
-    CHECK(fork.has_value());
-    CHECK_EQ(fork->len(), 64u);
-    // the borrower prefills the rest of its prompt from position 64
-    std::vector<uint32_t> rest(full.begin() + 64, full.end());
-    fork->reserve(full.size()).expect("room");
-    for (size_t i = 0; i < rest.size(); i++) {
-        const size_t pos = 64 + i;
+    fork.reserve(full.size()).expect("room");
+    for (size_t pos = 64; pos < full.size(); pos++) {
         for (size_t layer = 0; layer < N_LAYERS; layer++) {
             std::vector<float> k(KV_DIM), v(KV_DIM);
             for (size_t d = 0; d < KV_DIM; d++) {
                 k[d] = (float)full[pos] + (float)layer * 0.5f + (float)d * 0.125f;
                 v[d] = k[d] + 100.0f;
             }
-            fork->write(layer, pos, k.data(), v.data());
+            fork.write(layer, pos, k.data(), v.data());
         }
-        fork->advance();
+        fork.advance();
     }
     PagedKvCache cold = filled(shared, full);
     const AttnShape shape{(uint32_t)(2 * N_KV_HEADS), (uint32_t)N_KV_HEADS, (uint32_t)HEAD_DIM, 0.05f, 0.0f};
     Rng rng(91);
     const auto q = rng.normal(2 * N_KV_HEADS * HEAD_DIM);
     for (size_t layer = 0; layer < N_LAYERS; layer++) {
-        auto a = backend().decode_batch({{&*fork, 0, full.size()}}, q.data(), layer, shape).expect("fork");
+        auto a = backend().decode_batch({{&fork, 0, full.size()}}, q.data(), layer, shape).expect("fork");
         auto b = backend().decode_batch({{&cold, 0, full.size()}}, q.data(), layer, shape).expect("cold");
         CHECK(rows_equal(a, b));
     }
