@@ -104,6 +104,7 @@ SIGNATURES = {
     "gla_get_stream": (_P, [_P]),
     "gla_sync": (_I, [_P]),
     "gla_device_cu_count": (_I, [_P]),
+    "gla_release_stream": (_I, [_P, _P]),
     "gla_dev_alloc": (_I, [_P, _SZ, C.POINTER(_P)]),
     "gla_dev_free": (_I, [_P, _P]),
     "gla_memcpy_htod": (_I, [_P, _P, _P, _SZ]),

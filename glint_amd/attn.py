@@ -17,6 +17,7 @@ Every call goes to the HIP library; there is no CPU fallback here.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from typing import Optional, Sequence
 
 import numpy as np
@@ -266,6 +267,9 @@ class HipStream:
         s = C.c_void_p()
         _hip_check(_hip().hipStreamCreateWithFlags(C.byref(s), 1), "hipStreamCreateWithFlags")
         self.ptr = s
+        # backends that have run work on this stream: destroy() hands their
+        # scratch for it back (gla_release_stream) before the stream goes
+        self._users = weakref.WeakSet()
 
     @property
     def handle(self) -> int:
@@ -275,7 +279,13 @@ class HipStream:
         _hip_check(_hip().hipStreamSynchronize(self.ptr), "hipStreamSynchronize")
 
     def destroy(self) -> None:
+        """Release the stream: each backend that used it goes back to its own stream if this one
+        is current, and frees the scratch it kept for this stream (gla_release_stream, which
+        waits for the stream first); then the stream is destroyed."""
         if self.ptr:
+            for be in list(self._users):
+                be._forget_stream(self)
+            self._users = weakref.WeakSet()
             _hip().hipStreamDestroy(self.ptr)
             self.ptr = C.c_void_p()
 
@@ -325,11 +335,15 @@ class GpuBackend:
         p = C.c_void_p()
         check(_lib.lib().gla_create(device, C.byref(p)))
         self.ctx = p
+        # the HipStream set with set_stream (None: the context's own): held so
+        # the stream outlives its use by the context
+        self._stream: Optional["HipStream"] = None
 
     def close(self) -> None:
         if self.ctx:
             _lib.lib().gla_destroy(self.ctx)
             self.ctx = C.c_void_p()
+        self._stream = None
 
     def __del__(self):
         try:
@@ -347,8 +361,22 @@ class GpuBackend:
 
     def set_stream(self, stream: Optional["HipStream"]) -> None:
         """Enqueue later calls on `stream` (None: the backend's own stream). Work on different
-        streams uses different scratch buffers, so calls may overlap across streams."""
+        streams uses different scratch buffers, so calls may overlap across streams. The backend
+        keeps `stream` alive while it is set; HipStream.destroy() resets the backend first."""
+        if stream is not None and not stream.ptr:
+            raise ValueError("set_stream: the HipStream was destroyed")
         check(_lib.lib().gla_set_stream(self.ctx, stream.ptr if stream is not None else None))
+        self._stream = stream
+        if stream is not None:
+            stream._users.add(self)
+
+    def _forget_stream(self, stream: "HipStream") -> None:
+        """`stream` is about to be destroyed: leave it if current, and free its scratch."""
+        if not self.ctx:
+            return
+        if self._stream is stream:
+            self.set_stream(None)
+        check(_lib.lib().gla_release_stream(self.ctx, stream.ptr))
 
     @property
     def cu_count(self) -> int:

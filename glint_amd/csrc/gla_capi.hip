@@ -72,6 +72,17 @@ int ensure_scratch(gla_ctx *ctx, size_t bytes, void **out) {
     gla_ctx::StreamScratch *ss = nullptr;
     for (auto &e : ctx->scratch)
         if (e.stream == ctx->stream) ss = &e;
+    if (!ss || bytes > ss->bytes) {
+        // growing allocates, which a stream capture does not allow: refuse
+        // clearly instead of failing inside hipMalloc
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        GLA_CHECK_HIP(hipStreamIsCapturing(ctx->stream, &cs), GLA_ERR_DEVICE);
+        if (cs != hipStreamCaptureStatusNone)
+            return set_error(GLA_ERR_INVALID,
+                             "this call needs %zu bytes of scratch on a stream being captured, which holds %zu: "
+                             "scratch must be sized before capture (run the same call once eagerly first)",
+                             bytes, ss ? ss->bytes : (size_t)0);
+    }
     if (!ss) {
         ctx->scratch.push_back({ctx->stream, nullptr, 0});
         ss = &ctx->scratch.back();
@@ -237,6 +248,22 @@ int gla_set_stream(gla_ctx *ctx, void *hip_stream) {
 }
 
 void *gla_get_stream(gla_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int gla_release_stream(gla_ctx *ctx, void *hip_stream) {
+    GLA_GUARD_BEGIN
+    GLA_REQUIRE(ctx, "gla_release_stream: ctx is NULL");
+    const hipStream_t st = hip_stream ? (hipStream_t)hip_stream : ctx->own_stream;
+    auto it = std::find_if(ctx->scratch.begin(), ctx->scratch.end(),
+                           [&](const gla_ctx::StreamScratch &e) { return e.stream == st; });
+    if (ctx->stream == st && st != ctx->own_stream) ctx->stream = ctx->own_stream;
+    if (it == ctx->scratch.end()) return GLA_OK;
+    GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
+    GLA_CHECK_HIP(hipStreamSynchronize(st), GLA_ERR_KERNEL);
+    if (it->ptr) (void)hipFree(it->ptr);
+    ctx->scratch.erase(it);
+    return GLA_OK;
+    GLA_GUARD_END
+}
 
 int gla_sync(gla_ctx *ctx) {
     GLA_REQUIRE(ctx, "gla_sync: ctx is NULL");

@@ -724,7 +724,7 @@ __device__ __forceinline__ void q8_item(const Q8Params &p, uint8_t (*slots)[kSlo
     constexpr int kThreads = kWaves * 64;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kvh = hx / p.n_hg;
     const int hg = hx - kvh * p.n_hg;
     const int g0 = hg * p.hpw;

@@ -85,14 +85,28 @@ int gla_destroy(gla_ctx *ctx);
  * its own device scratch (decode split partials, bf16 prefill tile images,
  * matvec activation pieces), so calls queued on different streams at once
  * never share it and may overlap; calls on one stream run in order as usual.
- * The context itself is not thread-safe: switch streams from one thread. */
+ * That scratch is held until gla_destroy or gla_release_stream. The stream
+ * must outlive its use by the context: switch away from it (or release it)
+ * before destroying it. The context itself is not thread-safe: switch
+ * streams from one thread. */
 int gla_set_stream(gla_ctx *ctx, void *hip_stream);
 /* The hipStream_t work is enqueued on. */
 void *gla_get_stream(gla_ctx *ctx);
+/* Free the device scratch the context keeps for `hip_stream` (split
+ * partials, tile images, matvec pieces), after waiting for that stream.
+ * Scratch is otherwise held per stream until gla_destroy, so a caller that
+ * makes a stream per request calls this before destroying each stream. If
+ * `hip_stream` is the current stream, the context first returns to its own
+ * stream. Graphs captured on `hip_stream` must not be replayed afterwards.
+ * Buffers that a stream's scratch outgrew stay allocated until gla_destroy
+ * (earlier graphs may address them). Releasing a stream the context never
+ * used is a no-op. */
+int gla_release_stream(gla_ctx *ctx, void *hip_stream);
 /* Wait for all work enqueued on the context's stream. */
 int gla_sync(gla_ctx *ctx);
 /* Number of compute units of the context's device (0 on error). */
 int gla_device_cu_count(gla_ctx *ctx);
+
 
 /* ---- device memory (for device-resident q / out / tables) --------------- */
 
@@ -212,11 +226,13 @@ int gla_decode(gla_ctx *ctx, const gla_decode_args *args);
  * partials live in a static device array of GLA_DECODE_NOALLOC_SCRATCH_BYTES
  * that each GPU the library runs on holds until the process ends (resolved
  * once per device by gla_create). A call whose partials need more returns
- * GLA_ERR_INVALID before anything is launched (at Llama-3-8B heads: B=64 at
- * 8,192 positions needs 5.3 MiB). Every call on one GPU shares that GPU's
- * array and leaves its partials in it: calls that overlap on one GPU (two
- * streams or two contexts) race. Nothing in it needs clearing: a call
- * writes every partial it reads. */
+ * GLA_ERR_INVALID before anything is launched. The capacity depends on the
+ * storage: at Llama-3-8B heads (32/8, d128) and 8,192 positions per
+ * sequence, Q8_0 storage takes up to 192 sequences per call (B=64 needs
+ * 5.3 MiB), f32 storage up to 29 (f32 splits are shorter: 33 partials per
+ * KV head against 5). Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (two streams or two contexts) race. Nothing in it
+ * needs clearing: a call writes every partial it reads. */
 int gla_decode_noalloc(gla_ctx *ctx, const gla_decode_args *args);
 
 /* Batched causal prefill: query row r of sequence b sits at absolute

@@ -99,3 +99,29 @@ def test_graph_replays_equal_eager_calls(backend):
         g.destroy()
         w.destroy()
         big.destroy()
+
+
+def test_capture_that_would_grow_scratch_is_refused(backend):
+    """A captured call whose scratch the stream has not yet sized is refused with
+    GLA_ERR_INVALID (an allocation is not allowed inside a capture); the stream works after."""
+    from glint_amd.attn import HipStream
+    be = backend
+    w = be.create_q8_weights(orc.q8_quantize_rows(synth.normal_rows(17, 256, 1024)).reshape(-1), 256, 1024)
+    s = HipStream()
+    try:
+        be.set_stream(s)
+        x, y = be.buffer(synth.normal_rows(18, 64, 1024)), be.empty(64 * 256 * 4)
+        with pytest.raises(GlaError, match="sized before capture"):
+            be.capture(lambda: be.matvec_q8_0(w, x, 64, y))
+        be.matvec_q8_0(w, x, 64, y)  # eager: sizes the stream's scratch
+        be.sync()
+        g = be.capture(lambda: be.matvec_q8_0(w, x, 64, y))
+        want = y.download((64 * 256,)).copy()
+        g.replay()
+        be.sync()
+        assert np.array_equal(y.download((64 * 256,)).view(np.uint32), want.view(np.uint32))
+        g.destroy()
+    finally:
+        be.set_stream(None)
+        s.destroy()
+        w.destroy()

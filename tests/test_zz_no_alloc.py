@@ -74,20 +74,34 @@ def test_noalloc_equals_decode_f32(backend):
         assert np.array_equal(ref, got), n
 
 
-def test_noalloc_refuses_more_than_its_scratch(backend):
-    """512 sequences of up to 8,192 positions at Llama-3-8B heads need ~42 MB of partials:
-    GLA_ERR_INVALID, nothing launched; the next call works."""
-    H, Hkv, d, B = 32, 8, 128, 512
-    pool = backend.create_page_pool(64, Hkv, d, "q8")
+PARTIAL_BYTES = GLA_DECODE_NOALLOC_SCRATCH_BYTES
+
+
+@pytest.mark.parametrize("dtype,fits", [("q8", 192), ("f32", 29)])
+def test_noalloc_capacity_per_storage(backend, dtype, fits):
+    """The header's capacity at Llama-3-8B heads and 8,192 positions (no host lengths, so the
+    launch is sized from max_kv_len): `fits` sequences run and equal gla_decode bit for bit;
+    one more needs more partials than the array holds: GLA_ERR_INVALID, nothing launched; the
+    next call works. (Every table entry names page 0 of a small pool: the sizing, not the
+    data, is under test.)"""
+    H, Hkv, d = 32, 8, 128
+    pool = backend.create_page_pool(64, Hkv, d, dtype)
+    pool.write_rows(np.arange(16, dtype=np.int64), synth.normal_rows(9401, 16, Hkv * d),
+                    synth.normal_rows(9402, 16, Hkv * d))
     stride = 8192 // 16 + 1
-    table = backend.buffer(np.zeros((B, stride), np.int32))
-    zeros = backend.buffer(np.zeros(B, np.int32))
-    full = backend.buffer(np.full(B, 8192, np.int32))
-    q, out = backend.empty(B * H * d * 4), backend.empty(B * H * d * 4)
-    with pytest.raises(GlaError) as ei:
-        backend.decode(pool, q, out, zeros, full, B, 8192, H, 0.088, page_table=table, page_table_stride=stride,
-                       noalloc=True)
-    assert ei.value.code == GLA_ERR_INVALID
-    assert "scratch" in str(ei.value) and str(GLA_DECODE_NOALLOC_SCRATCH_BYTES) in str(ei.value)
-    pool.destroy()
+    try:
+        for B in (fits + 1, fits):
+            table = np.zeros((B, stride), np.int32)
+            starts, lens = np.zeros(B, np.int32), np.full(B, 8192, np.int32)
+            q = synth.normal(9403, (B, H, d))
+            if B > fits:
+                with pytest.raises(GlaError) as ei:
+                    _both(backend, pool, q, starts, lens, H, 0.088, table=table, host=False)
+                assert ei.value.code == GLA_ERR_INVALID
+                assert "scratch" in str(ei.value) and str(PARTIAL_BYTES) in str(ei.value)
+            else:
+                ref, got = _both(backend, pool, q, starts, lens, H, 0.088, table=table, host=False)
+                assert np.array_equal(ref, got)
+    finally:
+        pool.destroy()
     test_noalloc_equals_decode_f32(backend)
