@@ -195,6 +195,49 @@ __device__ __forceinline__ float wave_max(float x) {
     return x;
 }
 
+typedef int int16s __attribute__((ext_vector_type(16)));
+
+// Physical page of chunk page `lane` (0..npg-1) of sequence b, clamped into
+// the pool as map_page does, read through the scalar cache. A new
+// workgroup's first K/V loads wait for these ids: on the vector path the
+// table read queued behind the CU's streaming loads (1.7-3.3 us for
+// workgroups that start mid-kernel), on the scalar path it returns in
+// 0.2-0.3 us. Each round reads two 16-entry windows of the sequence's table
+// row with s_load_dwordx16, each window kept inside the row (a window that
+// would pass the row's end starts earlier instead), writes them into lanes
+// 0-15 of two registers and moves each chunk page's entry to its lane.
+// Needs pt_stride >= 16.
+__device__ __forceinline__ int chunk_ids_scalar(const PageMap &pm, int b, int pg0, int npg, int lane) {
+    const int32_t *row = pm.page_table + (int64_t)b * pm.pt_stride;
+    int v = 0;
+#pragma unroll
+    for (int g = 0; g < 64; g += 32) {
+        if (g >= npg) break;
+        const int w0 = min(pg0 + g, pm.pt_stride - 16);
+        const int w1 = min(pg0 + g + 16, pm.pt_stride - 16);
+        int16s lo, hi;
+        asm volatile(
+            "s_load_dwordx16 %0, %2, 0x0\n\t"
+            "s_load_dwordx16 %1, %3, 0x0\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&s"(lo), "=&s"(hi)
+            : "s"(row + w0), "s"(row + w1)
+            : "memory");
+        int tl = 0, th = 0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(tl) : "s"(lo[j]), "i"(j));
+            asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(th) : "s"(hi[j]), "i"(j));
+        }
+        const int a = __shfl(tl, min(max(pg0 + lane - w0, 0), 15));
+        const int c = __shfl(th, min(max(pg0 + lane - w1, 0), 15));
+        v = (lane >= g && lane < g + 16) ? a : v;
+        v = (lane >= g + 16 && lane < g + 32) ? c : v;
+    }
+    const int last = (int)(pm.n_pages - 1);
+    return v < 0 ? 0 : (v > last ? last : v);
+}
+
 // e with x = m * 2^e, m in [0.5, 1); scaling by 2^(14 - e) maps max|.| below 2^14.
 __device__ __forceinline__ int pow2_exp(float x) {
     int e = 0;
@@ -566,8 +609,43 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
         }
     }
     // physical page of chunk page `lane` (clamped into the pool by map_page)
-    const int pid_l = (int)map_page(p.pm, b, pg0 + min(lane, npg - 1));
+    const int pid_l = p.pm.page_table && p.pm.pt_stride >= 16
+                          ? chunk_ids_scalar(p.pm, b, pg0, npg, lane)
+                          : (int)map_page(p.pm, b, pg0 + min(lane, npg - 1));
     const uint8_t *head_base = p.base + (int64_t)kvh * p.head_stride;
+
+    // Start streaming the first step and request the chunk's V scales now,
+    // before q is split: the compiler does not count the streaming loads, so
+    // its wait for q below waits for them too, and the q, the step's K/V and
+    // the scales then arrive in one round trip.
+    const uint32_t slot_lds = __builtin_amdgcn_readfirstlane(lds_addr(slot));
+    issue_half<D, 0>(p, head_base, pid_l, 0, npg, lane, slot_lds);
+    issue_half<D, 1>(p, head_base, pid_l, 0, npg, lane, slot_lds);
+
+    // ---- largest V scale of the chunk: P' = p * vscale * 2^kv stays below 2^14 ----
+    // 16-byte units of the chunk's V scales, four loads per lane in flight per
+    // batch (one batch up to 128 pages at d128)
+    const int units = npg * 2 * NB;
+    auto scan_loads = [&](int u0, uint4 (&w)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int uu = min(u0 + j * 64 + lane, units - 1);
+            const int pid = __shfl(pid_l, uu / (2 * NB));
+            w[j] = *reinterpret_cast<const uint4 *>(head_base + (int64_t)pid * p.page_stride + 33 * D +
+                                                    (uu % (2 * NB)) * 16);
+        }
+    };
+    auto scan_max = [&](const uint4 (&w)[4], float vmax) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t a[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) vmax = fmaxf(vmax, fabsf(half_at(a, i)));
+        }
+        return vmax;
+    };
+    uint4 w0[4];
+    scan_loads(0, w0);
 
     // ---- Q as the B operand of S = K.Q ----
     float qx[NB][8];
@@ -599,34 +677,13 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
         }
     const float inv_qs = ldexpf(1.0f, qe - 14);
 
-    // start streaming the first step; the V-scale scan overlaps it. (The
-    // q split above comes first: the compiler does not count these loads, so
-    // a wait it placed for q after them would wait for them as well.)
-    const uint32_t slot_lds = __builtin_amdgcn_readfirstlane(lds_addr(slot));
-    issue_half<D, 0>(p, head_base, pid_l, 0, npg, lane, slot_lds);
-    issue_half<D, 1>(p, head_base, pid_l, 0, npg, lane, slot_lds);
-
-    // ---- largest V scale of the chunk: P' = p * vscale * 2^kv stays below 2^14 ----
     float inv_vsc;
     {
-        float vmax = 0.0f;
-        const int units = npg * 2 * NB;  // 16-byte units of the chunk's V scales
-        // four loads per lane in flight per batch (one batch up to 128 pages at d128)
-        for (int u0 = 0; u0 < units; u0 += 256) {
+        float vmax = scan_max(w0, 0.0f);
+        for (int u0 = 256; u0 < units; u0 += 256) {
             uint4 w[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int uu = min(u0 + j * 64 + lane, units - 1);
-                const int pid = __shfl(pid_l, uu / (2 * NB));
-                w[j] = *reinterpret_cast<const uint4 *>(head_base + (int64_t)pid * p.page_stride + 33 * D +
-                                                        (uu % (2 * NB)) * 16);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t a[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
-#pragma unroll
-                for (int i = 0; i < 8; i++) vmax = fmaxf(vmax, fabsf(half_at(a, i)));
-            }
+            scan_loads(u0, w);
+            vmax = scan_max(w, vmax);
         }
         vmax = wave_max(vmax);
         const int ve = pow2_exp(vmax);
