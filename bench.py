@@ -33,8 +33,9 @@ on this host with gcc -O3 -march=native -ffp-contract=off, on the same inputs,
 on a bounded sample: one thread for configs 1 and 2 (Glint's single-sequence
 decode is serial over heads, src/transformer/forward.rs:254-269), otherwise
 parallel over sequences (forward.rs:1499-1502) or query positions
-(forward.rs:927-931) on the cores this process may use, at most 16 (a GPU
-box's CPU share). `cores` is the thread count; `host_cores` what the process
+(forward.rs:927-931) on the cores this process may use (Rayon's default
+width), fewer only if OMP_NUM_THREADS says so (a shared host's CPU share).
+`cores` is the thread count; `host_cores` what the process
 could see.
 
 errors: the GPU output for the cpu_baseline sample (the same call, after the
@@ -570,39 +571,6 @@ def achievable(be: GpuBackend) -> dict:
                    "N(0,1) operands (glint_amd/csrc/gla_probe.hip)"}
 
 
-PREFILL_PATTERN_MODES = {
-    0: "tiles + MFMAs only (no q loads, no output stores, no softmax)",
-    2: "+ f32 output stores",
-    8: "+ output stores into an L2-resident 32 KB buffer",
-    1: "+ f32 q loads",
-    9: "+ q loads and output stores into the L2-resident buffer",
-    3: "+ q loads and output stores",
-    7: "+ q loads, output stores and a minimal softmax",
-    16: "mode 0 on random N(0,1) inputs (the others run on near-constant inputs)",
-    19: "mode 3 on random inputs",
-    23: "mode 7 on random inputs",
-}
-
-
-def prefill_structure() -> dict:
-    """The staged bf16 prefill kernel's pattern over the cfg4 grid with parts switched on and off
-    (glint_amd/csrc/gla_probe.hip, prefill_pattern_kernel): microseconds per launch, best of 5."""
-    import ctypes as C
-    lib = C.CDLL(str(ROOT / "glint_amd" / "libglint_probe.so"))
-    lib.glp_prefill_pattern.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double)]
-    flops = 4 * 32 * 2 * 2 * 128 * (2048 * 2049 // 2)
-    out = {}
-    for mode, what in PREFILL_PATTERN_MODES.items():
-        us = C.c_double()
-        rc = lib.glp_prefill_pattern(mode, 5, C.byref(us))
-        if rc != 0:
-            raise RuntimeError(f"glp_prefill_pattern({mode}) failed ({rc})")
-        out[f"mode_{mode}"] = {"what": what, "us": round(us.value, 1),
-                               "TFLOP_per_s": round(flops / (us.value * 1e-6) / 1e12, 1)}
-        log(f"prefill pattern mode {mode}: {us.value:.1f} us ({what})")
-    return out
-
-
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -613,8 +581,6 @@ def main() -> int:
     ap.add_argument("--calibrate", action="store_true", help="also run known-size page copies (for PMC runs)")
     ap.add_argument("--achievable", action="store_true",
                     help="measure the achievable ceilings also when one workload is selected")
-    ap.add_argument("--prefill-structure", action="store_true",
-                    help="also time the staged bf16 prefill's pattern with parts switched off (gla_probe)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU: the attention path has no multi-GPU leg "
@@ -801,9 +767,6 @@ def main() -> int:
     if args.calibrate:
         log("calibration copies")
         result["calibration"] = calibrate(be)
-    if args.prefill_structure:
-        log("prefill pattern probe (cfg4 grid)")
-        result["prefill_structure"] = prefill_structure()
     if pending:
         log("CPU baselines and errors (oracle, same inputs as each leg's sample)")
     for wl, kw, sample, tol, place in pending:

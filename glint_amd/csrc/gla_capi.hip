@@ -636,6 +636,19 @@ static int decode_launch_of(gla_ctx *ctx, const gla_decode_args *a, const char *
                 "%s: pass both kv_start_host and kv_len_host, or neither", fn);
     d->kv_start_host = a->kv_start_host;
     d->kv_len_host = a->kv_len_host;
+    if (a->kv_len_host) {
+        // The reference panics on a window outside the storage
+        // (src/cache/paged.rs:453-465, src/cache/mod.rs:167-171); with the
+        // host copies this is seen before anything is launched.
+        const int64_t limit = d->pm.pos_limit;
+        for (int b = 0; b < a->n_seqs; b++) {
+            const int64_t st = a->kv_start_host[b], len = a->kv_len_host[b];
+            GLA_REQUIRE(st >= 0 && len >= 0 && len <= a->max_kv_len && st + len <= limit,
+                        "%s: sequence %d attends positions [%lld, %lld), outside [0, %lld) or longer than "
+                        "max_kv_len %d",
+                        fn, b, (long long)st, (long long)(st + len), (long long)limit, a->max_kv_len);
+        }
+    }
     GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
     if (a->kv_len_host) {
         // The host lengths size the launch; a captured graph would replay

@@ -186,7 +186,23 @@ long gla_window_start(long pos, long sliding_window, int alternating, int layer)
  * KV, K/V head h / (n_heads / n_kv_heads), cap(s) = softcap * tanh(s / softcap)
  * when softcap > 0 -- flash_attn_1d_ext per head (src/tensor/flash.rs:46-124)
  * as attn_heads_cpu calls it (src/transformer/forward.rs:240-270). kv_len 0
- * gives a zero output, as the reference's pre-zeroed buffer does. */
+ * gives a zero output, as the reference's pre-zeroed buffer does.
+ *
+ * Out-of-range indices. The reference panics on a position or page id
+ * outside the storage (Vec indexing in PagedKvCache::read_k_head,
+ * src/cache/paged.rs:453-465; the write/truncate bounds of
+ * src/cache/mod.rs:167-171, :186-190). Here:
+ *   - with the host copies (kv_start_host / kv_len_host), every window is
+ *     checked on the host before anything is launched: kv_start < 0,
+ *     kv_len < 0, kv_len > max_kv_len, or kv_start + kv_len past the
+ *     storage (the cache's max_seq; a pool's page_table_stride * 16
+ *     positions) returns GLA_ERR_INVALID and the next call works;
+ *   - the device arrays themselves are not read by the host. The kernels
+ *     clamp every index they derive from them into the storage (positions
+ *     to [0, storage positions), seq_slot to [0, n_seqs of the cache), page
+ *     ids to [0, pages of the pool)), so a malformed device length, slot or
+ *     page-table entry gives attention over the clamped positions and
+ *     GLA_OK, never an access outside the storage. */
 typedef struct gla_decode_args {
     const gla_kv *kv;          /* contiguous cache or pool */
     int layer;                 /* contiguous caches: layer to read; ignored for pools */
@@ -241,7 +257,15 @@ int gla_decode_noalloc(gla_ctx *ctx, const gla_decode_args *args);
  * when sliding_window > 0 else 0 -- the loop of src/transformer/forward.rs:927-958
  * (pass sliding_window = 0 for a global layer of an alternating model). The
  * K/V of every attended position must already be written, as the reference
- * writes the chunk before attending (forward.rs:874-877). */
+ * writes the chunk before attending (forward.rs:874-877).
+ *
+ * Out-of-range indices, as for gla_decode: the attended key positions are
+ * clamped into the storage (a pos_offset past it attends the stored
+ * positions only; a negative one attends none of its own) and seq_slot and
+ * page-table entries into the cache or pool, so a malformed device value
+ * gives clamped attention and GLA_OK where the reference would panic. The
+ * query rows q_start[b] .. q_start[b+1]-1 index q and out, whose size the
+ * library is not told: they must lie inside those buffers. */
 typedef struct gla_prefill_args {
     const gla_kv *kv;
     int layer;

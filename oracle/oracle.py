@@ -102,8 +102,14 @@ def host_cores() -> int:
 
 
 def threads() -> int:
-    """Worker threads: the cores this process may use, at most 16 (a GPU box's CPU share)."""
-    return max(1, min(16, host_cores()))
+    """Worker threads: the cores this process may use (its affinity mask, what Rust's
+    available_parallelism() and so Rayon's default pool see), unless OMP_NUM_THREADS asks for
+    fewer (a shared host's CPU share; the GPU boxes set it to their share)."""
+    n = host_cores()
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
 
 
 def _p(a: np.ndarray) -> C.c_void_p:

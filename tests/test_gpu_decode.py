@@ -318,3 +318,37 @@ def test_q8_host_lengths_beyond_the_row_list(backend, monkeypatch):
     b = run_decode(backend, p.pool, q, pb.kv_start, pb.kv_len, H, 0.125, table=pb.table, host_lengths=False)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     assert_close(a, want, what="q8 host lengths past the row list")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+def test_host_lengths_outside_the_storage_are_refused(backend, dtype):
+    """The reference panics on a window outside the storage (src/cache/paged.rs:453-465,
+    src/cache/mod.rs:167-171). With the host copies of the lengths, gla_decode refuses such a
+    window on the host (GLA_ERR_INVALID) before anything runs; the out buffer is untouched and the
+    next call works."""
+    from glint_amd._lib import GLA_ERR_INVALID, GlaError
+    H, Hkv, d = 8, 2, 64
+    ctx = np.array([100, 40, 333], np.int32)
+    pb = synth.paged_batch(851, ctx)
+    p = Pool(backend, dtype, pb, Hkv, d, seed=852)
+    q = synth.normal(853, (len(ctx), H, d))
+    limit = pb.table.shape[1] * 16  # positions a row of the page table covers
+    dq, dout = backend.buffer(np.ascontiguousarray(q)), backend.buffer(np.full(q.shape, 7.0, np.float32))
+    table = backend.buffer(np.ascontiguousarray(pb.table))
+    bad = [
+        (np.array([0, 0, limit - 10], np.int32), np.array([100, 40, 11], np.int32), limit),  # past the end
+        (np.array([0, -1, 0], np.int32), np.array([100, 40, 333], np.int32), 333),           # negative start
+        (np.array([0, 0, 0], np.int32), np.array([100, -3, 333], np.int32), 333),            # negative length
+        (np.array([0, 0, 0], np.int32), np.array([100, 40, 333], np.int32), 300),            # > max_kv_len
+    ]
+    for st, ln, max_len in bad:
+        ds, dl = backend.buffer(st), backend.buffer(ln)
+        with pytest.raises(GlaError) as ei:
+            backend.decode(p.pool, dq, dout, ds, dl, len(ctx), max_len, H, 0.125, None, page_table=table,
+                           page_table_stride=pb.table.shape[1], kv_start_host=st, kv_len_host=ln)
+        assert ei.value.code == GLA_ERR_INVALID and "outside" in str(ei.value)
+    backend.sync()
+    assert np.all(dout.download(q.shape) == 7.0)  # nothing ran
+    want = _oracle_decode(p.stores, q, pb.kv_start, pb.kv_len, H, Hkv, d, 0.125)
+    got = run_decode(backend, p.pool, q, pb.kv_start, pb.kv_len, H, 0.125, table=pb.table)
+    assert_close(got, want, what=f"{dtype} after the refusals")
