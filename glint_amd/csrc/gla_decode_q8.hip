@@ -905,12 +905,16 @@ __global__ __launch_bounds__(kWaves * 64) void decode_q8_mfma_kernel(const Q8Par
 }
 
 // Merge of the workgroup partials of every unit with more than one
-// workgroup; grid (kGT*D/256, KV head x head group, sequence).
+// workgroup; grid (KV head x head group, sequence), kGT*D/4 threads, each
+// merging four consecutive elements of one head (16-byte loads of the
+// partials; the per-element arithmetic is that of a scalar merge: eight
+// partials at a time, all loads of a batch in flight together, (M, L, A)
+// absorbing the batch with one rescale).
 template <int D>
-__global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p) {
-    const int b = blockIdx.z;
-    const int kvh = blockIdx.y / p.n_hg;
-    const int hg = blockIdx.y - kvh * p.n_hg;
+__global__ __launch_bounds__(kGT * D / 4) void decode_q8_combine_kernel(const Q8Params p) {
+    const int b = blockIdx.y;
+    const int kvh = blockIdx.x / p.n_hg;
+    const int hg = blockIdx.x - kvh * p.n_hg;
     const int g0 = hg * p.hpw;
     const int gcount = min(p.hpw, p.group - g0);
     const int h_base = kvh * p.group + g0;
@@ -918,24 +922,23 @@ __global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p
     const int span = kWaves * p.ch;  // pages per workgroup
     const int n_wg = min((r.n_pages + span - 1) / span, p.max_wg);
     if (n_wg <= 1) return;
-    const int idx = blockIdx.x * 256 + threadIdx.x;
-    const int g = idx / D;
-    const int d = idx - g * D;
+    const int g = (4 * (int)threadIdx.x) / D;
+    const int d = 4 * (int)threadIdx.x - g * D;
     if (g >= gcount) return;
     const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
     constexpr int64_t pstride = kPartStride<D>;
     const float *hp = p.part + unit * p.max_wg * pstride;
-    // one pass, eight partials at a time: all loads of a batch are in flight
-    // together, and (M, L, A) absorb the batch with one rescale
-    float M = -INFINITY, L = 0.0f, A = 0.0f;
+    float M = -INFINITY, L = 0.0f;
+    float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int i0 = 0; i0 < n_wg; i0 += 8) {
-        float mi[8], li[8], ai[8];
+        float mi[8], li[8];
+        float4 ai[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int i = min(i0 + j, n_wg - 1);
             mi[j] = (i0 + j < n_wg) ? hp[i * pstride + kGT * D + g] : -INFINITY;
             li[j] = hp[i * pstride + kGT * D + kGT + g];
-            ai[j] = hp[i * pstride + g * D + d];
+            ai[j] = *reinterpret_cast<const float4 *>(hp + i * pstride + g * D + d);
         }
         float bm = M;
 #pragma unroll
@@ -943,16 +946,24 @@ __global__ __launch_bounds__(256) void decode_q8_combine_kernel(const Q8Params p
         if (bm == -INFINITY) continue;
         const float f0 = (M == -INFINITY) ? 0.0f : fast_exp2(M - bm);
         L *= f0;
-        A *= f0;
+        A.x *= f0;
+        A.y *= f0;
+        A.z *= f0;
+        A.w *= f0;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const float f = (mi[j] == -INFINITY) ? 0.0f : fast_exp2(mi[j] - bm);
             L = fmaf(li[j], f, L);
-            A = fmaf(ai[j], f, A);
+            A.x = fmaf(ai[j].x, f, A.x);
+            A.y = fmaf(ai[j].y, f, A.y);
+            A.z = fmaf(ai[j].z, f, A.z);
+            A.w = fmaf(ai[j].w, f, A.w);
         }
         M = bm;
     }
-    p.out[((int64_t)b * p.n_heads + h_base + g) * D + d] = L > 0.0f ? A * (1.0f / L) : 0.0f;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    *reinterpret_cast<float4 *>(p.out + ((int64_t)b * p.n_heads + h_base + g) * D + d) =
+        L > 0.0f ? make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 template <int D>
@@ -961,8 +972,8 @@ int launch_d(gla_ctx *ctx, const Q8Params &prm, dim3 grid, int n_seqs) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "decode_q8_mfma_kernel launch: %s", hipGetErrorString(e));
     if (prm.max_wg > 1) {
-        hipLaunchKernelGGL((decode_q8_combine_kernel<D>), dim3(kGT * D / 256, grid.x, n_seqs), dim3(256), 0,
-                           ctx->stream, prm);
+        hipLaunchKernelGGL((decode_q8_combine_kernel<D>), dim3(prm.n_kv_heads * prm.n_hg, n_seqs), dim3(kGT * D / 4),
+                           0, ctx->stream, prm);
         e = hipGetLastError();
         if (e != hipSuccess)
             return set_error(GLA_ERR_KERNEL, "decode_q8_combine_kernel launch: %s", hipGetErrorString(e));
