@@ -92,6 +92,53 @@ int ensure_scratch(gla_ctx *ctx, size_t bytes, void **out) {
     return rc;
 }
 
+int decode_arrivals(gla_ctx *ctx, const DecodeLaunch &d, size_t n, int32_t **out) {
+    *out = nullptr;
+    if (d.scratch) {
+        if (n > d.arrivals_cap)
+            return set_error(GLA_ERR_INVALID,
+                             "decode needs %zu arrival counters (sequences x KV heads x head groups); the fixed "
+                             "array holds %zu",
+                             n, d.arrivals_cap);
+        *out = d.arrivals;
+        return GLA_OK;
+    }
+    gla_ctx::StreamScratch *ss = nullptr;
+    for (auto &e : ctx->scratch)
+        if (e.stream == ctx->stream) ss = &e;
+    if (ss && n <= ss->n_arrivals) {
+        *out = ss->arrivals;
+        return GLA_OK;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    GLA_CHECK_HIP(hipStreamIsCapturing(ctx->stream, &cs), GLA_ERR_DEVICE);
+    if (cs != hipStreamCaptureStatusNone)
+        return set_error(GLA_ERR_INVALID,
+                         "this call needs %zu arrival counters on a stream being captured, which holds %zu: they "
+                         "must be sized before capture (run the same call once eagerly first)",
+                         n, ss ? ss->n_arrivals : (size_t)0);
+    if (!ss) {
+        ctx->scratch.push_back({ctx->stream, nullptr, 0});
+        ss = &ctx->scratch.back();
+    }
+    const size_t want = std::max<size_t>(n, std::max<size_t>(1024, 2 * ss->n_arrivals));
+    void *fresh = nullptr;
+    hipError_t e = hipMalloc(&fresh, want * sizeof(int32_t));
+    if (e != hipSuccess)
+        return set_error(GLA_ERR_BUFFER, "allocation of %zu arrival counters failed: %s", want, hipGetErrorString(e));
+    // (queued on the stream: ordered before every launch that uses them)
+    e = hipMemsetAsync(fresh, 0, want * sizeof(int32_t), ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(fresh);
+        return set_error(GLA_ERR_DEVICE, "zeroing the arrival counters failed: %s", hipGetErrorString(e));
+    }
+    if (ss->arrivals) ctx->retired.emplace_back(ss->arrivals, false);
+    ss->arrivals = (int32_t *)fresh;
+    ss->n_arrivals = want;
+    *out = ss->arrivals;
+    return GLA_OK;
+}
+
 int decode_scratch(gla_ctx *ctx, const DecodeLaunch &d, size_t bytes, void **out) {
     if (!d.scratch) return ensure_scratch(ctx, bytes, out);
     *out = nullptr;
@@ -114,21 +161,30 @@ static bool head_dim_ok(int d) { return d == 64 || d == 128 || d == 256; }
 // process ends. In host code `scratch` is only a stand-in for the symbol;
 // kernels get the device address gla_create resolved for the device.
 static __device__ __align__(256) uint8_t scratch[GLA_DECODE_NOALLOC_SCRATCH_BYTES];
+// Its arrival counters (zero-initialised when the code object loads; every
+// call leaves them at zero). Same stand-in rule as `scratch`.
+static __device__ __align__(256) int32_t scratch_arrivals[GLA_DECODE_NOALLOC_UNITS];
 
 constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static void *g_scratch_ptr[kMaxDevices];
+static void *g_arrivals_ptr[kMaxDevices];
 static hipError_t g_scratch_err[kMaxDevices];
 
-// Resolve `scratch` on `device` (which must be current), once per device.
+// Resolve `scratch` and `scratch_arrivals` on `device` (which must be
+// current), once per device.
 static void resolve_scratch(int device) {
     if (device < 0 || device >= kMaxDevices) return;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch_ptr[device]) return;
-    void *ptr = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    void *ptr = nullptr, *arr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) e = hipGetSymbolAddress(&arr, HIP_SYMBOL(scratch_arrivals));
     g_scratch_err[device] = e;
-    if (e == hipSuccess) g_scratch_ptr[device] = ptr;
+    if (e == hipSuccess) {
+        g_scratch_ptr[device] = ptr;
+        g_arrivals_ptr[device] = arr;
+    }
 }
 
 // The device address of `device`'s array, or NULL with the error set.
@@ -143,6 +199,10 @@ static void *scratch_of(int device) {
         set_error(GLA_ERR_DEVICE, "gla_decode_noalloc: the static scratch of device %d has no address (%s)", device,
                   hipGetErrorString(g_scratch_err[device]));
     return g_scratch_ptr[device];
+}
+static int32_t *arrivals_of(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return (device >= 0 && device < kMaxDevices) ? (int32_t *)g_arrivals_ptr[device] : nullptr;
 }
 
 // Waits for the context's stream when it goes out of scope unless released:
@@ -219,8 +279,10 @@ int gla_destroy(gla_ctx *ctx) {
     if (!ctx) return GLA_OK;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    for (const auto &e : ctx->scratch)
+    for (const auto &e : ctx->scratch) {
         if (e.ptr) (void)hipFree(e.ptr);
+        if (e.arrivals) (void)hipFree(e.arrivals);
+    }
     for (gla_kv *kv : ctx->kvs) {
         if (kv->base) (void)hipFree(kv->base);
         kv->base = nullptr;
@@ -260,6 +322,7 @@ int gla_release_stream(gla_ctx *ctx, void *hip_stream) {
     GLA_CHECK_HIP(hipSetDevice(ctx->device), GLA_ERR_DEVICE);
     GLA_CHECK_HIP(hipStreamSynchronize(st), GLA_ERR_KERNEL);
     if (it->ptr) (void)hipFree(it->ptr);
+    if (it->arrivals) (void)hipFree(it->arrivals);
     ctx->scratch.erase(it);
     return GLA_OK;
     GLA_GUARD_END
@@ -682,6 +745,8 @@ int gla_decode_noalloc(gla_ctx *ctx, const gla_decode_args *a) {
     d.scratch = scratch_of(ctx->device);
     if (!d.scratch) return GLA_ERR_DEVICE;
     d.scratch_cap = GLA_DECODE_NOALLOC_SCRATCH_BYTES;
+    d.arrivals = arrivals_of(ctx->device);
+    d.arrivals_cap = GLA_DECODE_NOALLOC_UNITS;
     return launch_decode(ctx, d);
     GLA_GUARD_END
 }

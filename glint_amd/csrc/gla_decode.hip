@@ -35,6 +35,9 @@ constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kStepsPerIter = 2;  // half-page token steps a lane group loads per iteration
+// Windows of at most this many pages merge their splits in the last
+// workgroup to finish instead of a combine launch.
+constexpr int kMergePages = 64;
 
 struct DecodeParams {
     KvLayout kv;
@@ -54,6 +57,12 @@ struct DecodeParams {
     int max_len;  // host bound on kv_len: lengths are clamped to it, so splits never exceed max_splits
     float q_mul;    // multiplier of q.k: scale*log2(e), or scale with a soft-cap
     float softcap;  // > 0: cap * tanh(s / cap)
+    // Windows of at most merge_pages pages (and more than one split) are
+    // merged by the last of their workgroups to finish, counted in
+    // arrivals[unit] (0 between calls: the last arrival resets it); longer
+    // windows by decode_combine_kernel.
+    int merge_pages;
+    int32_t *arrivals;
 };
 
 // Sum over the 8 lanes of an aligned lane group (DPP: quad xor1, quad xor2,
@@ -156,6 +165,56 @@ __device__ __forceinline__ uint4 load_nt(const uint8_t *p) {
 
 __device__ __forceinline__ float word_f(const uint4 &c, int w) {
     return __uint_as_float(w == 0 ? c.x : (w == 1 ? c.y : (w == 2 ? c.z : c.w)));
+}
+
+// Agent-scope (all XCDs) accesses of the partials a unit merges in its last
+// workgroup: they bypass the per-XCD L2s, which are not coherent with each
+// other within a kernel.
+__device__ __forceinline__ void store_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until every memory access this thread issued has completed (its
+// agent-scope stores have reached the memory all XCDs share).
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// Merge of the splits of one unit's head g, element e, in split order, eight
+// splits at a time ((M, L, A) absorbing each batch with one rescale): the
+// last-arriving workgroup's merge of a short window.
+template <int D, int GT>
+__device__ __forceinline__ float merge_splits_agent(const DecodeParams &p, int64_t slot0, int n_splits, int g, int e) {
+    float M = -INFINITY, L = 0.0f, A = 0.0f;
+    for (int s0 = 0; s0 < n_splits; s0 += 8) {
+        float mi[8], li[8], ai[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int s = min(s0 + j, n_splits - 1);
+            mi[j] = load_agent(p.part_ml + (slot0 + s) * 32 + g);
+            li[j] = load_agent(p.part_ml + (slot0 + s) * 32 + 8 + g);
+            ai[j] = load_agent(p.part_acc + ((slot0 + s) * GT + g) * D + e);
+        }
+        const int nv = n_splits - s0;
+        float bm = M;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (j < nv) bm = fmaxf(bm, mi[j]);
+        const float f0 = (M == -INFINITY) ? 0.0f : fast_exp2(M - bm);
+        L *= f0;
+        A *= f0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (j < nv) {
+                const float f = (mi[j] == -INFINITY) ? 0.0f : fast_exp2(mi[j] - bm);
+                L = fmaf(li[j], f, L);
+                A = fmaf(ai[j], f, A);
+            }
+        }
+        M = bm;
+    }
+    return L > 0.0f ? A * (1.0f / L) : 0.0f;
 }
 
 template <int D, int GT, int NSTEP, bool CAP>
@@ -349,6 +408,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
 
     // merge the 4 waves; write the output or this split's partial
     const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
+    const bool arrive = r.n_splits > 1 && r.n_pages <= p.merge_pages;  // a rule on the window alone
     for (int idx = tid; idx < gcount * D; idx += kThreads) {
         const int g = idx / D;
         const int e = idx - g * D;
@@ -367,7 +427,10 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
             p.out[((int64_t)b * p.n_heads + h_base + g) * D + e] = L > 0.0f ? A * (1.0f / L) : 0.0f;
         } else {
             const int64_t slot = unit * p.max_splits + split;
-            p.part_acc[(slot * GT + g) * D + e] = A;
+            if (arrive)
+                store_agent(p.part_acc + (slot * GT + g) * D + e, A);
+            else
+                p.part_acc[(slot * GT + g) * D + e] = A;
         }
     }
     // (m, l) of the split's heads as one whole 128-byte line: sub-line writes cost a
@@ -394,7 +457,32 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
             v[j] = tid < 2 ? m_s : (tid < 4 ? l_s : 0.0f);
         }
         const int64_t slot = unit * p.max_splits + split;
-        *reinterpret_cast<float4 *>(p.part_ml + slot * 32 + 4 * tid) = make_float4(v[0], v[1], v[2], v[3]);
+        if (arrive) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) store_agent(p.part_ml + slot * 32 + 4 * tid + j, v[j]);
+        } else {
+            *reinterpret_cast<float4 *>(p.part_ml + slot * 32 + 4 * tid) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    if (!arrive) return;
+    // Short window: count this split's arrival once all of its partial has
+    // reached shared memory; the unit's last workgroup merges every split.
+    __shared__ int lds_last;
+    wait_vm_all();
+    __syncthreads();
+    if (tid == 0) {
+        const int before = __hip_atomic_fetch_add(p.arrivals + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = before == r.n_splits - 1;
+        if (last) __hip_atomic_store(p.arrivals + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lds_last = last;
+    }
+    __syncthreads();
+    if (!lds_last) return;
+    const int64_t slot0 = unit * p.max_splits;
+    for (int idx = tid; idx < gcount * D; idx += kThreads) {
+        const int g = idx / D;
+        const int e = idx - g * D;
+        p.out[((int64_t)b * p.n_heads + h_base + g) * D + e] = merge_splits_agent<D, GT>(p, slot0, r.n_splits, g, e);
     }
 }
 
@@ -417,7 +505,7 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(const DecodePa
     const int gcount = min(GT, p.group - hg * GT);
     if (g >= gcount) return;
     const SeqRange r = seq_range(p, b);
-    if (r.n_splits <= 1) return;
+    if (r.n_splits <= 1 || r.n_pages <= p.merge_pages) return;  // (short windows merge in the split kernel)
     const int sg = threadIdx.x / RL;
     const int e4 = threadIdx.x - sg * RL;
     const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
@@ -575,8 +663,36 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
     const bool cap = d.softcap > 0.0f;
     prm.q_mul = cap ? d.scale : d.scale * kLog2e;
     prm.softcap = cap ? d.softcap : 0.0f;
+    // Windows of up to kMergePages pages merge their splits in the split
+    // kernel's last workgroup (no combine launch); GLA_DECODE_MERGE_PAGES
+    // sets another bound (tuning only; 0: every window through the combine).
+    int merge_pages = kMergePages;
+    if (const char *env = getenv("GLA_DECODE_MERGE_PAGES")) merge_pages = std::max(0, atoi(env));
+    prm.merge_pages = merge_pages;
+    prm.arrivals = nullptr;
+    // Which merges the launch needs: exact from the host lengths, else from
+    // the max_kv_len bound.
+    bool any_short = false, any_long = false;
+    if (d.kv_len_host) {
+        for (int b = 0; b < d.n_seqs; b++) {
+            const int n = host_seq_pages(d.kv_start_host[b], d.kv_len_host[b], d.max_kv_len, d.pm.pos_limit);
+            const int pps = pps_fixed > 0 ? pps_fixed : split_pages(n);
+            if ((n + pps - 1) / pps <= 1) continue;
+            if (n <= merge_pages)
+                any_short = true;
+            else
+                any_long = true;
+        }
+    } else {
+        any_short = max_splits > 1 && merge_pages > 0;
+        any_long = max_splits > 1 && max_pages > merge_pages;
+    }
     prm.part_acc = nullptr;
     prm.part_ml = nullptr;
+    if (any_short) {
+        int rc = decode_arrivals(ctx, d, (size_t)units, &prm.arrivals);
+        if (rc != GLA_OK) return rc;
+    }
     if (max_splits > 1) {
         const size_t slots = (size_t)units * max_splits;
         const size_t acc_b = slots * gt * D * sizeof(float);
@@ -592,11 +708,11 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
     dim3 grid(d.n_kv_heads * n_hg, max_splits, d.n_seqs);
     switch (D) {
     case 64:
-        return launch_d<64>(ctx, gt, prm, grid, max_splits > 1);
+        return launch_d<64>(ctx, gt, prm, grid, any_long);
     case 128:
-        return launch_d<128>(ctx, gt, prm, grid, max_splits > 1);
+        return launch_d<128>(ctx, gt, prm, grid, any_long);
     case 256:
-        return launch_d<256>(ctx, gt, prm, grid, max_splits > 1);
+        return launch_d<256>(ctx, gt, prm, grid, any_long);
     }
     return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
 }

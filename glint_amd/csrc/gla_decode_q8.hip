@@ -994,16 +994,6 @@ int resident_wgs() {
     return cached;
 }
 
-// Pages the window of one sequence spans, with seq_range's clamping.
-int host_seq_pages(int start, int len, int max_len, int pos_limit) {
-    start = start < 0 ? 0 : start;
-    len = len < 0 ? 0 : (len > max_len ? max_len : len);
-    int64_t e = (int64_t)start + len;
-    if (e > pos_limit) e = pos_limit;
-    const int64_t s = start > e ? e : start;
-    return e > s ? (int)(((e - 1) >> 4) - (s >> 4) + 1) : 0;
-}
-
 // Pages per chunk: 28 (14 steps) for head_dim up to 128, 40 for 256, for
 // every window (a chunk holds at most 64 pages, one page id per lane).
 // Measured on the Llama-3-8B and Gemma-2-9B batch decodes with the workgroups

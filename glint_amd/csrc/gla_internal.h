@@ -126,6 +126,10 @@ struct gla_ctx {
         hipStream_t stream;
         void *ptr;
         size_t bytes;
+        // arrival counters of the f32 decode's in-kernel merge: zeroed when
+        // allocated, and every call leaves them at zero
+        int32_t *arrivals = nullptr;
+        size_t n_arrivals = 0;
     };
     std::vector<StreamScratch> scratch;
     // device and pinned host staging of the host-pointer entry points
@@ -178,6 +182,17 @@ int ensure_dstage(gla_ctx *ctx, size_t bytes);
 void detach_q8w(gla_q8w *w);
 int ensure_hstage(gla_ctx *ctx, size_t bytes);
 
+// Pages the window of one sequence spans, with the decode kernels' clamping
+// of its start and length (their seq_range), from the host copies.
+inline int host_seq_pages(int start, int len, int max_len, int pos_limit) {
+    start = start < 0 ? 0 : start;
+    len = len < 0 ? 0 : (len > max_len ? max_len : len);
+    int64_t e = (int64_t)start + len;
+    if (e > pos_limit) e = pos_limit;
+    const int64_t s = start > e ? e : start;
+    return e > s ? (int)(((e - 1) >> 4) - (s >> 4) + 1) : 0;
+}
+
 // Launchers (return GLA_OK or an error code with the message set).
 struct DecodeLaunch {
     KvLayout kv;
@@ -201,10 +216,17 @@ struct DecodeLaunch {
     // partials need more; when NULL the context's scratch is used.
     void *scratch = nullptr;
     size_t scratch_cap = 0;
+    // with `scratch`: a fixed array of arrivals_cap arrival counters (zero
+    // between calls), else the context's counters for its current stream
+    int32_t *arrivals = nullptr;
+    size_t arrivals_cap = 0;
 };
 // Device scratch of a decode launch: d.scratch (no allocation) or the
 // context's buffer for its current stream.
 int decode_scratch(gla_ctx *ctx, const DecodeLaunch &d, size_t bytes, void **out);
+// At least n zeroed arrival counters for a decode launch (d.arrivals, or the
+// context's for its current stream).
+int decode_arrivals(gla_ctx *ctx, const DecodeLaunch &d, size_t n, int32_t **out);
 int launch_decode(gla_ctx *ctx, const DecodeLaunch &d);
 int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d);
 

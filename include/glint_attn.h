@@ -234,6 +234,10 @@ int gla_decode(gla_ctx *ctx, const gla_decode_args *args);
 
 /* Device scratch gla_decode_noalloc may use, in bytes (one array per GPU). */
 #define GLA_DECODE_NOALLOC_SCRATCH_BYTES (16u << 20)
+/* (sequence, KV head, head group) units an f32-storage gla_decode_noalloc
+ * call may hold (arrival counters of the short-window merge; one array per
+ * GPU). */
+#define GLA_DECODE_NOALLOC_UNITS 65536
 
 /* gla_decode that allocates nothing. It has no counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph
@@ -248,7 +252,11 @@ int gla_decode(gla_ctx *ctx, const gla_decode_args *args);
  * 5.3 MiB), f32 storage up to 29 (f32 splits are shorter: 33 partials per
  * KV head against 5). Every call on one GPU shares that GPU's array: calls
  * that overlap on one GPU (two streams or two contexts) race. Nothing in it
- * needs clearing: a call writes every partial it reads. */
+ * needs clearing: a call writes every partial it reads. f32 windows of at
+ * most 64 pages merge their splits in the last workgroup to finish and count
+ * arrivals in a second static array of GLA_DECODE_NOALLOC_UNITS counters
+ * (zero when the library loads, left at zero by every call); a call with
+ * more (sequence, KV head, head group) units returns GLA_ERR_INVALID. */
 int gla_decode_noalloc(gla_ctx *ctx, const gla_decode_args *args);
 
 /* Batched causal prefill: query row r of sequence b sits at absolute

@@ -71,3 +71,39 @@ def test_decode_is_batch_invariant_cfg3(backend, cfg3_batch, dtype):
                     assert np.array_equal(_bits(got), _bits(full[b].reshape(-1))), f"attention() seq {b}"
     finally:
         pool.destroy()
+
+
+@pytest.mark.parametrize("d,h,hkv", [(64, 9, 3), (128, 32, 8)])
+def test_f32_merge_switch_is_batch_invariant(backend, d, h, hkv):
+    """f32 windows of up to 64 pages merge their splits in the split kernel's last workgroup to
+    arrive; longer ones in decode_combine_kernel. The choice is a rule on the window alone, so
+    windows on both sides of it (64 and 65 pages, from a page boundary and from mid-page, plus
+    one-split windows) give the same bits alone, in a batch that mixes both merges, in a shuffled
+    sub-batch and with the launch sized without host lengths; each matches the oracle, and the
+    arrival counters are left ready for the next call (a second run repeats the bits)."""
+    import oracle as orc
+    from gpu_util import Contig
+    from helpers import assert_close
+
+    starts = np.array([0, 0, 0, 0, 0, 8, 8, 0, 5, 3], np.int32)
+    lens = np.array([1, 16, 17, 63 * 16, 64 * 16, 64 * 16 - 8, 64 * 16 - 7, 65 * 16, 2000, 130], np.int32)
+    B = len(lens)
+    c = Contig(backend, "f32", B, 1, int((starts + lens).max()), hkv, d, seed=5150 + d)
+    q = synth.normal(5151 + d, (B, h, d))
+    scale = float(1 / np.sqrt(d))
+    want = orc.decode_batch(q.reshape(B, h * d), c.stores, 0, starts, lens, h, hkv, d, scale,
+                            None).reshape(B, h, d)
+    full = run_decode(backend, c.cache, q, starts, lens, h, scale)
+    assert_close(full, want, what=f"d{d} batch across the merge switch")
+    again = run_decode(backend, c.cache, q, starts, lens, h, scale)
+    assert np.array_equal(_bits(again), _bits(full)), "second call"
+    nohost = run_decode(backend, c.cache, q, starts, lens, h, scale, host_lengths=False)
+    assert np.array_equal(_bits(nohost), _bits(full)), "launch sized without host lengths"
+    sub = np.random.default_rng(5152).permutation(B)[:6]
+    part = run_decode(backend, c.cache, q[sub], starts[sub], lens[sub], h, scale, seq_slot=sub)
+    for i, b in enumerate(sub):
+        assert np.array_equal(_bits(part[i]), _bits(full[b])), f"seq {b} in a shuffled sub-batch"
+    for b in range(B):
+        alone = run_decode(backend, c.cache, q[b:b + 1], starts[b:b + 1], lens[b:b + 1], h, scale,
+                           seq_slot=[b])
+        assert np.array_equal(_bits(alone[0]), _bits(full[b])), f"seq {b} (start {starts[b]}, len {lens[b]}) alone"
