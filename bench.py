@@ -21,6 +21,17 @@ per-step times ("timing_us"); rates use the median. Consecutive steps
 alternate between layers whose K/V live in different memory, so the 256 MB
 Infinity Cache cannot serve repeats.
 
+Settle. A leg's set-up (pool writes, uploads, host work) leaves the GPU
+mostly idle for a while, and the first ~100 calls after such a gap run
+through the power controller's transient: at cfg3 (K=50) the median was
+108.4-109.0 us against 101.6-101.9 us in sustained work, bf16 prefill
+185-192 us against 158-162 us. So right before each leg's W warmup steps the
+bench runs a different kernel of the leg's kind -- ~0.1 s of streaming reads
+of a 1 GiB buffer for the HBM-bound legs, ~0.3 s of the bf16 MFMA loop on
+random operands for the prefill legs (glint_amd/csrc/gla_probe.hip) -- and
+the timed steps measure what the path sustains. The W warmup and K timed steps are the leg's own, unchanged;
+"settle" in the JSON says what ran.
+
 roofline: algorithmic bytes of one call (unique K/V bytes of the attended
 positions, page-table entries, q and out) divided by the call's median
 duration; the call is decode_q8_mfma_kernel + decode_q8_combine_kernel.
@@ -547,17 +558,54 @@ def traffic_from_profile() -> tuple[int | None, str | None]:
 
 
 # --------------------------------------------------------------------------- main
-def achievable(be: GpuBackend) -> dict:
-    """Ceilings measured on this GPU (glint_amd/csrc/gla_probe.hip): a 2 GiB streaming read with
-    non-temporal loads, and MFMA-only loops for fp32 (16x16x4) and bf16 (16x16x32)."""
-    import ctypes as C
+def probe_lib():
     lib = C.CDLL(str(ROOT / "glint_amd" / "libglint_probe.so"))
     lib.glp_stream_read.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.POINTER(C.c_double)]
     lib.glp_mfma_peak.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double)]
+    return lib
+
+
+class Settle:
+    """A kernel of the leg's kind right before its warmup (see the module docstring): "hbm"
+    streams a 1 GiB buffer 625 times with non-temporal loads (~0.1 s at 7 TB/s); "mfma" runs
+    the bf16 MFMA-only loop on random N(0,1) operands for 550,000 iterations (~0.3 s), whose
+    power draw is closest to the prefill's (the near-constant-operand loop, or 0.08 s, left
+    the next calls 1-3% slower)."""
+
+    HOW = {"hbm": "625 streaming reads of a 1 GiB buffer (glp_stream_read), ~0.1 s",
+           "mfma": "bf16 MFMA-only loop on random operands, 550,000 iterations (glp_mfma_peak mode 2), ~0.3 s"}
+
+    def __init__(self, be: GpuBackend):
+        self.lib = probe_lib()
+        self.buf = be.empty(1 << 30)
+
+    def __call__(self, kind: str) -> str:
+        out = C.c_double()
+        if kind == "hbm":
+            rc = self.lib.glp_stream_read(self.buf.ptr, 1 << 30, 625, C.byref(out))
+        else:
+            rc = self.lib.glp_mfma_peak(2, 550000, C.byref(out))
+        if rc != 0:
+            raise RuntimeError(f"gla_probe settle call failed ({rc})")
+        return kind
+
+    def close(self):
+        self.buf.free()
+
+
+def achievable(be: GpuBackend, settle: Settle) -> dict:
+    """Ceilings measured on this GPU (glint_amd/csrc/gla_probe.hip): a 2 GiB streaming read with
+    non-temporal loads, and MFMA-only loops for fp32 (16x16x4) and bf16 (16x16x32), each after a
+    settle of its kind."""
+    lib = settle.lib
     nbytes = 2 << 30
     buf = be.empty(nbytes)
     gbs, f32, bf16, bf16r, f32r = C.c_double(), C.c_double(), C.c_double(), C.c_double(), C.c_double()
-    for rc in (lib.glp_stream_read(buf.ptr, nbytes, 10, C.byref(gbs)),
+    settle("hbm")
+    rc = lib.glp_stream_read(buf.ptr, nbytes, 10, C.byref(gbs))
+    if rc == 0:
+        settle("mfma")
+    for rc in (rc,
                lib.glp_mfma_peak(0, 50000, C.byref(f32)), lib.glp_mfma_peak(1, 50000, C.byref(bf16)),
                lib.glp_mfma_peak(2, 50000, C.byref(bf16r)), lib.glp_mfma_peak(3, 50000, C.byref(f32r))):
         if rc != 0:
@@ -568,7 +616,7 @@ def achievable(be: GpuBackend) -> dict:
             "fp32_mfma_random_data_tflops": round(f32r.value, 1),
             "how": "2 GiB streaming read with non-temporal 16-byte loads; MFMA-only loops, 8 waves per CU, "
                    "8 independent accumulators per wave, on near-constant operands and on random "
-                   "N(0,1) operands (glint_amd/csrc/gla_probe.hip)"}
+                   "N(0,1) operands (glint_amd/csrc/gla_probe.hip); each after a settle of its kind"}
 
 
 def main() -> int:
@@ -601,9 +649,11 @@ def main() -> int:
     }
     secondary = {}
     ach = None
+    settle = Settle(be)
+    result["settle"] = {"before": "each leg's warmup, after its set-up", **Settle.HOW}
     if args.workload == "all" or args.achievable:
         log("achievable ceilings (streaming read, MFMA loops)")
-        ach = achievable(be)
+        ach = achievable(be, settle)
         result["achievable"] = ach
 
     def frac_of(value, key):
@@ -624,6 +674,7 @@ def main() -> int:
     if "cfg3" in want:
         log("cfg3: paged Q8_0 pool, 2 layers, B=64")
         wl = PagedDecode(be, "cfg3", 32, 8, 128, 64, 128, 8192, 256, None, [None, None], 1.0, SEED + 3)
+        settled = settle("hbm")
         t = time_steps(be, ev, wl.step, steps, args.warmup)
         ms = t.median_ms
         gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
@@ -644,7 +695,7 @@ def main() -> int:
             "frac_of_achievable": frac_of(gbs, "hbm_read_gbs"),
             "kernel": "decode_q8_mfma_kernel<128> + decode_q8_combine_kernel<128> (one gla_decode call)",
             "algorithmic_bytes_per_call": int(wl.bytes_per_step()),
-            "us_per_call": round(ms * 1e3, 2), "timing_us": t.summary_us(),
+            "us_per_call": round(ms * 1e3, 2), "timing_us": t.summary_us(), "settle": settled,
         }
         if src:
             result["roofline"]["traffic_source"] = src
@@ -657,6 +708,7 @@ def main() -> int:
     if "cfg5" in want:
         log("cfg5: Gemma-2 paged Q8_0 pool (windowed + global layer)")
         wl = PagedDecode(be, "cfg5", 16, 8, 256, 32, 2048, 8192, 0, 50.0, [4096, None], 3.0, SEED + 5)
+        settled = settle("hbm")
         t = time_steps(be, ev, wl.step, steps, args.warmup)
         ms = t.median_ms
         gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
@@ -665,7 +717,7 @@ def main() -> int:
                         "global layers alternating (one step = one layer)",
             "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2), "timing_us": t.summary_us(),
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs")}
+            "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs"), "settle": settled}
         defer(wl, lambda base, ref, errors, e=e: e.update(cpu_baseline=base, errors=errors),
               min_seconds=5.0, max_reps=10)
         log(f"cfg5: {ms * 1e3:.1f} us/layer, {gbs:.1f} GB/s")
@@ -673,6 +725,7 @@ def main() -> int:
     if "cfg2" in want:
         log("cfg2: 32-layer f32 cache")
         wl = ContigDecode(be, 32, 4096, 32, 8, 128, 0x2222, "cfg2")
+        settled = settle("hbm")
         t = time_steps(be, ev, wl.step, steps, args.warmup, group=wl.n_layers)
         ms = t.median_ms
         gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
@@ -680,30 +733,32 @@ def main() -> int:
             "workload": "Llama-3-8B single-sequence decode, f32 contiguous ctx 4096, 32 layers back to back",
             "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2), "timing_us": t.summary_us(),
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs")}
+            "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs"), "settle": settled}
         defer(wl, lambda base, ref, errors, e=e: e.update(cpu_baseline=base, errors=errors))
         log(f"cfg2: {ms * 1e3:.1f} us/layer, {gbs:.1f} GB/s")
         del wl
     if "cfg1" in want:
         log("cfg1: SmolLM-135M decode, f32 ctx 512")
         wl = ContigDecode(be, 8, 512, 9, 3, 64, 0x1111, "cfg1")
+        settled = settle("hbm")
         t = time_steps(be, ev, wl.step, steps, args.warmup, group=wl.n_layers)
         ms = t.median_ms
         e = secondary["cfg1"] = {
             "workload": "SmolLM-135M decode, H9/KV3 d64, B=1, f32 contiguous ctx 512 (latency)",
             "value": round(ms * 1e3, 2), "unit": "us/call", "timing_us": t.summary_us(),
-            "GB_per_s": round(wl.bytes_per_step() / (ms * 1e-3) / 1e9, 2)}
+            "GB_per_s": round(wl.bytes_per_step() / (ms * 1e-3) / 1e9, 2), "settle": settled}
         log(f"cfg1: {ms * 1e3:.2f} us/call")
         # the same layers' calls captured as one HIP graph (a decode step's attention), replayed:
         # the launch cost of a call is then paid once per step, not once per kernel
         g = be.capture(lambda: [wl.step(i) for i in range(wl.n_layers)])
+        settled = settle("hbm")
         t = time_steps(be, ev, lambda i: g.replay(), steps, args.warmup, group=4)
         ms_g = t.median_ms / wl.n_layers
         g.destroy()
         secondary["cfg1_graph"] = {
             "workload": f"cfg1, the {wl.n_layers} layers' gla_decode calls captured as one HIP graph and replayed",
             "value": round(ms_g * 1e3, 2), "unit": "us/call", "timing_us_per_replay": t.summary_us(),
-            "GB_per_s": round(wl.bytes_per_step() / (ms_g * 1e-3) / 1e9, 2)}
+            "GB_per_s": round(wl.bytes_per_step() / (ms_g * 1e-3) / 1e9, 2), "settle": settled}
         log(f"cfg1 graph: {ms_g * 1e3:.2f} us/call")
         defer(wl, lambda base, ref, errors, e=e: e.update(cpu_baseline=base, errors=errors),
               min_seconds=2.0, max_reps=20000)
@@ -711,42 +766,49 @@ def main() -> int:
     if "cfg4" in want:
         log("cfg4: 4x2048 causal prefill, f32 KV cache")
         wl = Prefill(be)
-        t = time_steps(be, ev, wl.step, steps, args.warmup)
-        ms = t.median_ms
-        tf = wl.flops_per_step() / (ms * 1e-3) / 1e12
-        e = secondary["cfg4_f32"] = {
-            "workload": "Llama-3-8B causal prefill 4x2048, f32 KV cache, fp32-input MFMA",
-            "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "timing_us": t.summary_us(),
-            "frac_of_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
-            "frac_of_achievable_fp32_mfma": frac_of(tf, "fp32_mfma_tflops"),
-            "frac_of_achievable_fp32_mfma_random_data": frac_of(tf, "fp32_mfma_random_data_tflops")}
-        e_f32 = e
-        sample_f32 = wl.gpu_sample() if cb is not None else None
-        log(f"cfg4 f32: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
-        # bf16-input variant: same inputs rounded to bf16 inside the kernel
+        # bf16-input variant first: the fp32 leg's ~60 ms of full-rate MFMA work just before it
+        # left its calls 2-5% slower than after its own settle alone
         wl.precision = "bf16"
+        settled = settle("mfma")
         t = time_steps(be, ev, wl.step, steps, args.warmup)
         ms = t.median_ms
         tf = wl.flops_per_step() / (ms * 1e-3) / 1e12
-        e = secondary["cfg4_bf16"] = {
+        e_bf16 = secondary["cfg4_bf16"] = {
             "workload": "Llama-3-8B causal prefill 4x2048, f32 KV cache, bf16-input MFMA (fp32 accumulate)",
             "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "timing_us": t.summary_us(),
             "frac_of_bf16_mfma_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
             "frac_of_achievable_bf16_mfma": frac_of(tf, "bf16_mfma_tflops"),
             "frac_of_achievable_bf16_mfma_random_data": frac_of(tf, "bf16_mfma_random_data_tflops"),
-            "tolerance": "max abs 3e-2 / rel 3e-2 vs the fp32 oracle (tests/test_gpu_prefill.py)"}
+            "tolerance": "max abs 3e-2 / rel 3e-2 vs the fp32 oracle (tests/test_gpu_prefill.py)",
+            "settle": settled}
+        log(f"cfg4 bf16: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
+        wl.precision = "f32"
+        settled = settle("mfma")
+        t = time_steps(be, ev, wl.step, steps, args.warmup)
+        ms = t.median_ms
+        tf = wl.flops_per_step() / (ms * 1e-3) / 1e12
+        e_f32 = secondary["cfg4_f32"] = {
+            "workload": "Llama-3-8B causal prefill 4x2048, f32 KV cache, fp32-input MFMA",
+            "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "timing_us": t.summary_us(),
+            "frac_of_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+            "frac_of_achievable_fp32_mfma": frac_of(tf, "fp32_mfma_tflops"),
+            "frac_of_achievable_fp32_mfma_random_data": frac_of(tf, "fp32_mfma_random_data_tflops"),
+            "settle": settled}
+        sample_f32 = wl.gpu_sample() if cb is not None else None
+        log(f"cfg4 f32: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
         # one CPU leg for both precisions (the same sample inputs): the bf16 output against the
         # fp32 oracle at the bf16 bar, the fp32 output (taken above) at the fp32 bar
-        def place_cfg4(base, ref, errors, e_bf16=e, e_f32=e_f32, sample_f32=sample_f32):
+        def place_cfg4(base, ref, errors, e_bf16=e_bf16, e_f32=e_f32, sample_f32=sample_f32):
             e_f32.update(cpu_baseline=base, errors=error_figures(sample_f32, ref, 1e-4, 1e-3))
             e_bf16["errors"] = errors
+        wl.precision = "bf16"  # the deferred sample is the bf16 output
         defer(wl, place_cfg4, tol=(3e-2, 3e-2))
-        log(f"cfg4 bf16: {ms:.3f} ms/step, {tf:.1f} TFLOP/s")
         del wl
     if "proj" in want:
         for n_vec in (1, 64):
             log(f"proj: Q8_0 QKV matvec, {n_vec} token(s)")
             wl = ProjMatvec(be, n_vec)
+            settled = settle("hbm")
             t = time_steps(be, ev, wl.step, steps, args.warmup, group=len(wl.w))
             ms = t.median_ms
             gbs = wl.bytes_per_step() / (ms * 1e-3) / 1e9
@@ -756,7 +818,7 @@ def main() -> int:
                             f"rotation), {n_vec} token(s) per call (gla_matvec_q8_0)",
                 "value": round(gbs, 2), "unit": "GB/s", "us_per_call": round(ms * 1e3, 2),
                 "timing_us": t.summary_us(), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-                "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs")}
+                "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs"), "settle": settled}
             def place_proj(base, ref, errors, e=e, n_vec=n_vec):
                 e["errors"] = errors
                 if n_vec == 1:
@@ -781,6 +843,7 @@ def main() -> int:
     if secondary:
         result["secondary"] = secondary
     print(json.dumps(result), flush=True)
+    settle.close()
     be.close()
     return 0
 
