@@ -103,6 +103,11 @@ int decode_arrivals(gla_ctx *ctx, const DecodeLaunch &d, size_t n, int32_t **out
         *out = d.arrivals;
         return GLA_OK;
     }
+    return ensure_arrivals(ctx, n, out);
+}
+
+int ensure_arrivals(gla_ctx *ctx, size_t n, int32_t **out) {
+    *out = nullptr;
     gla_ctx::StreamScratch *ss = nullptr;
     for (auto &e : ctx->scratch)
         if (e.stream == ctx->stream) ss = &e;

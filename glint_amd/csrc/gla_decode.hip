@@ -167,20 +167,6 @@ __device__ __forceinline__ float word_f(const uint4 &c, int w) {
     return __uint_as_float(w == 0 ? c.x : (w == 1 ? c.y : (w == 2 ? c.z : c.w)));
 }
 
-// Agent-scope (all XCDs) accesses of the partials a unit merges in its last
-// workgroup: they bypass the per-XCD L2s, which are not coherent with each
-// other within a kernel.
-__device__ __forceinline__ void store_agent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(const float *p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Wait until every memory access this thread issued has completed (its
-// agent-scope stores have reached the memory all XCDs share).
-__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
-
 // Merge of the splits of one unit's head g, element e, in split order, eight
 // splits at a time ((M, L, A) absorbing each batch with one rescale): the
 // last-arriving workgroup's merge of a short window.
@@ -468,16 +454,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
     // Short window: count this split's arrival once all of its partial has
     // reached shared memory; the unit's last workgroup merges every split.
     __shared__ int lds_last;
-    wait_vm_all();
-    __syncthreads();
-    if (tid == 0) {
-        const int before = __hip_atomic_fetch_add(p.arrivals + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = before == r.n_splits - 1;
-        if (last) __hip_atomic_store(p.arrivals + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        lds_last = last;
-    }
-    __syncthreads();
-    if (!lds_last) return;
+    if (!arrive_last(p.arrivals + unit, r.n_splits, &lds_last)) return;
     const int64_t slot0 = unit * p.max_splits;
     for (int idx = tid; idx < gcount * D; idx += kThreads) {
         const int g = idx / D;

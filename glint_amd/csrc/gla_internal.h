@@ -100,6 +100,36 @@ __host__ __device__ __forceinline__ int q8ks_off(int slot, int blk, int D) {
     return ((blk & 1) * 16 + slot) * (D >> 6) + (blk >> 1);
 }
 
+// Agent-scope (all XCDs) accesses of partials that the last workgroup to
+// arrive merges inside one kernel: they bypass the per-XCD L2s, which are
+// not coherent with each other within a kernel.
+__device__ __forceinline__ void store_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until every memory access this thread issued has completed (its
+// agent-scope stores have reached the memory all XCDs share).
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// One thread of the workgroup counts its arrival at counter *c once every
+// thread's stores have completed; true in every thread of the workgroup that
+// arrives last of n (which resets the counter to 0 for the next call).
+__device__ __forceinline__ bool arrive_last(int32_t *c, int n, int *lds_flag) {
+    wait_vm_all();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int before = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = before == n - 1;
+        if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *lds_flag = last;
+    }
+    __syncthreads();
+    return *lds_flag != 0;
+}
+
 __device__ __forceinline__ int64_t map_page(const PageMap &pm, int b, int lp) {
     int64_t id;
     if (pm.page_table) {
@@ -126,8 +156,8 @@ struct gla_ctx {
         hipStream_t stream;
         void *ptr;
         size_t bytes;
-        // arrival counters of the f32 decode's in-kernel merge: zeroed when
-        // allocated, and every call leaves them at zero
+        // arrival counters of the in-kernel merges (f32 decode, Q8_0 matvec
+        // K slices): zeroed when allocated, and every call leaves them at zero
         int32_t *arrivals = nullptr;
         size_t n_arrivals = 0;
     };
@@ -227,6 +257,10 @@ int decode_scratch(gla_ctx *ctx, const DecodeLaunch &d, size_t bytes, void **out
 // At least n zeroed arrival counters for a decode launch (d.arrivals, or the
 // context's for its current stream).
 int decode_arrivals(gla_ctx *ctx, const DecodeLaunch &d, size_t n, int32_t **out);
+// At least n zeroed arrival counters of the context for its current stream
+// (every kernel that counts arrivals leaves them at zero; kernels on one
+// stream run one after another, so they can share them).
+int ensure_arrivals(gla_ctx *ctx, size_t n, int32_t **out);
 int launch_decode(gla_ctx *ctx, const DecodeLaunch &d);
 int launch_decode_q8(gla_ctx *ctx, const DecodeLaunch &d);
 

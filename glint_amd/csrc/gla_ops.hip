@@ -143,28 +143,37 @@ __global__ __launch_bounds__(256) void q8w_repack_kernel(const uint8_t *ggml, in
 
 // ---- activations: f16 pieces ---------------------------------------------------
 
-// Grid (chunks of 256 * kSplitU units, padded vector count); vectors past
-// n_vec get zero pieces. Each thread holds its units' 8 elements each in
-// registers; the vector's largest |x| comes from those registers when one
-// chunk covers the vector (a second, streaming read otherwise), and the
-// pieces are written from the same registers, in the B-operand order of the
-// MFMA: xp[v / 16][blk][piece][lane = kg*16 + v % 16] = 8 f16 of elements
-// blk*32 + kg*8 .. +8 (piece 0 hi, 1 lo), so that one vector tile's piece of
-// a block is 1 KiB contiguous; xs[v] = 2^-s, the factor that undoes the
-// scaling.
-constexpr int kSplitU = 8;
+// Grid (chunks of kSplitChunk units, padded vector count / 4), 1024 threads:
+// a workgroup takes 4 consecutive vectors (thread t always vector t & 3) and
+// the units of its chunk, kSplitU per thread; vectors past n_vec get zero pieces. Each thread
+// holds its units' 8 elements each in registers; a vector's largest |x|
+// comes from those registers when one chunk covers the vector (a second,
+// streaming read otherwise), and the pieces are written from the same
+// registers, in the B-operand order of the MFMA: xp[v / 16][blk][piece][lane
+// = kg*16 + v % 16] = 8 f16 of elements blk*32 + kg*8 .. +8 (piece 0 hi, 1
+// lo), so that one vector tile's piece of a block is 1 KiB contiguous; xs[v]
+// = 2^-s, the factor that undoes the scaling. With 4 vectors per workgroup,
+// 4 consecutive lanes write 4 consecutive 16-byte pieces, one 64-byte
+// request (one vector per workgroup wrote each piece as a 32-byte request).
+constexpr int kSplitThreads = 1024;
+constexpr int kSplitU = 2;                                      // units per thread
+constexpr int kSplitV = 4;                                      // vectors per workgroup
+constexpr int kSplitStep = kSplitThreads / kSplitV;             // units of a vector per pass
+constexpr int kSplitChunk = kSplitU * kSplitStep;               // units per workgroup
 template <bool A16>  // x rows 16-byte aligned: float4 loads
-__global__ __launch_bounds__(256) void split_x_kernel(const float *x, int n_vec, int cols, int n_blocks_pad,
-                                                      _Float16 *xp, float *xs) {
-    const int v = blockIdx.y;
+__global__ __launch_bounds__(kSplitThreads) void split_x_kernel(const float *x, int n_vec, int cols,
+                                                                int n_blocks_pad, _Float16 *xp, float *xs) {
+    const int vq = threadIdx.x & (kSplitV - 1);
+    const int v = blockIdx.y * kSplitV + vq;
     const float *xv = x + (int64_t)min(v, n_vec - 1) * cols;
     const int n_units = n_blocks_pad * 4;
     const int cu = cols / 8;  // units inside the row (cols is a multiple of 32)
+    const int ut = threadIdx.x / kSplitV;  // the thread's unit within each pass
     float e[kSplitU][8];
     float mx = 0.0f;
 #pragma unroll
     for (int k = 0; k < kSplitU; k++) {
-        const int u = blockIdx.x * 256 * kSplitU + k * 256 + threadIdx.x;
+        const int u = blockIdx.x * kSplitChunk + k * kSplitStep + ut;
         const float *src = xv + (int64_t)min(u, cu - 1) * 8;  // clamped: loads stay in the row
         if (A16) {
             const float4 a = *reinterpret_cast<const float4 *>(src);
@@ -183,21 +192,26 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float *x, int n_vec,
         }
     }
     if (gridDim.x > 1 && v < n_vec) {  // rows wider than one chunk: the rest of the row's maximum
-        for (int c = threadIdx.x; c < cols; c += 256) mx = fmaxf(mx, fabsf(xv[c]));
+        for (int c = ut; c < cols; c += kSplitStep) mx = fmaxf(mx, fabsf(xv[c]));
     }
-    __shared__ float red[4];
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    // maximum over the threads of the same vector: lanes of equal t & 3 in
+    // the wave, then the waves
+    constexpr int NW = kSplitThreads / 64;
+    __shared__ float red[NW][kSplitV];
+    for (int o = kSplitV; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((threadIdx.x & 63) < kSplitV) red[threadIdx.x >> 6][vq] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0][vq];
+#pragma unroll
+    for (int w = 1; w < NW; w++) mx = fmaxf(mx, red[w][vq]);
     int ex = 0;
     if (mx > 0.0f && isfinite(mx)) frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
     const int sh = 14 - ex;                            // the largest |x| * 2^sh lies in [2^13, 2^14)
     const float mul = ldexpf(1.0f, sh);
-    if (blockIdx.x == 0 && threadIdx.x == 0) xs[v] = ldexpf(1.0f, -sh);
+    if (blockIdx.x == 0 && threadIdx.x < kSplitV) xs[v] = ldexpf(1.0f, -sh);
 #pragma unroll
     for (int k = 0; k < kSplitU; k++) {
-        const int u = blockIdx.x * 256 * kSplitU + k * 256 + threadIdx.x;
+        const int u = blockIdx.x * kSplitChunk + k * kSplitStep + ut;
         if (u >= n_units) break;
         half8 hi, lo;
 #pragma unroll
@@ -217,6 +231,16 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float *x, int n_vec,
 
 // ---- the matvec ----------------------------------------------------------------------
 
+// Four consecutive floats as two 8-byte agent-scope loads (bypassing the
+// per-XCD L2s, like load_agent; the compiler tracks them in its waits).
+__device__ __forceinline__ floatx4 load_agent4(const float *p) {
+    uint64_t *q = reinterpret_cast<uint64_t *>(const_cast<float *>(p));
+    const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return floatx4{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)), __uint_as_float((uint32_t)b),
+                   __uint_as_float((uint32_t)(b >> 32))};
+}
+
 // 4 bytes x + 128 -> 4 exact f16 (1024 + byte - 1152) at o[at .. at+3].
 __device__ __forceinline__ void bytes_to_h(uint32_t u, half8 &o, int at) {
     const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x07010700u);  // bytes 0, 1 under 0x64
@@ -234,7 +258,7 @@ __device__ __forceinline__ void bytes_to_h(uint32_t u, half8 &o, int at) {
 constexpr int kMaxVT = 4;        // vector tiles (16 vectors each) per launch
 constexpr int kSkWaves = 4;      // waves per workgroup: a quarter of the workgroup's blocks each
 constexpr int kSkRT = 4;         // row tiles per wave (and per workgroup): 64 rows share each x fragment
-constexpr int kSkMaxSplits = 8;  // K slices per launch (partials summed by matvec_reduce_kernel)
+constexpr int kSkMaxSplits = 8;  // K slices per launch (summed by each row group's last workgroup)
 constexpr int kSkTargetWgs = 512;
 
 // One K slice of y[v][row] for up to 64 vectors: workgroup (g, s) owns rows
@@ -242,13 +266,16 @@ constexpr int kSkTargetWgs = 512;
 // wave holds 4 row tiles x NVT vector tiles of accumulators, so every x
 // fragment it loads serves four row tiles and every weight fragment NVT
 // vector tiles. The waves are merged in LDS in a fixed order and the slice's
-// sums (times the vector's piece factor) go to out[s][vv][row], or straight
-// to y when there is one slice. Splitting K across workgroups is what keeps
+// sums (times the vector's piece factor) go to out[s][vv][row] as agent-scope
+// stores, or straight to y when there is one slice; the row group's last
+// workgroup to arrive (counted in arrivals[row group]) sums the slices into
+// y, so no reduce launch follows. Splitting K across workgroups is what keeps
 // the x fragments each CU reads to its slice of x, not all of it.
 template <int NVT>
 __global__ __launch_bounds__(kSkWaves * 64) void matvec_q8_splitk_kernel(
     const uint8_t *quants, const uint16_t *scales, int rows, int n_tiles, int n_pairs, const _Float16 *xp,
-    const float *xs, int n_blocks_pad, int v0, int n_vec, int n_splits, float *out, int64_t split_stride) {
+    const float *xs, int n_blocks_pad, int v0, int n_vec, int n_splits, float *out, int64_t split_stride, float *y,
+    int32_t *arrivals) {
     constexpr int RT = kSkRT;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -370,33 +397,65 @@ __global__ __launch_bounds__(kSkWaves * 64) void matvec_q8_splitk_kernel(
         for (int w = 1; w < kSkWaves; w++) sum += red[red_at(w, rt, vt, ln) + r];
         const int row = tile0 * 16 + rl;
         const int v = v0 + vv;
-        if (row < rows && v < n_vec) o[(int64_t)vv * rows + row] = sum * xsl[vv];
+        if (row < rows && v < n_vec) {
+            if (arrivals)
+                store_agent(o + (int64_t)vv * rows + row, sum * xsl[vv]);
+            else
+                o[(int64_t)vv * rows + row] = sum * xsl[vv];
+        }
     }
-}
-
-// y[vv][row] = sum over the slices s = 0, 1, .. of part[s][vv][row], in order
-// (all slices' loads in flight at once).
-__global__ __launch_bounds__(256) void matvec_reduce_kernel(const float *part, int n_splits, int64_t split_stride,
-                                                            int64_t n_out, float *y) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n_out) return;
-    float t[kSkMaxSplits];
+    if (!arrivals) return;
+    // K slices summed by the last of the row group's workgroups to arrive, in
+    // slice order: y = ((s0 + s1) + s2) + ..., the same sums whichever
+    // workgroup is last
+    __shared__ int lds_last;
+    if (!arrive_last(arrivals + blockIdx.x, n_splits, &lds_last)) return;
+    constexpr int NQ = RT * 16 * NVT * 16 / 4 / (kSkWaves * 64);  // row quads per thread
+    if (rows % 4 == 0 && ((uintptr_t)y & 15) == 0) {  // whole 16-byte row quads
+        floatx4 t[NQ][kSkMaxSplits];
 #pragma unroll
-    for (int s = 0; s < kSkMaxSplits; s++) t[s] = part[min(s, n_splits - 1) * split_stride + i];
-    float sum = t[0];
+        for (int k = 0; k < NQ; k++) {
+            const int qd = threadIdx.x + k * kSkWaves * 64;
+            const int rl = 4 * (qd & (RT * 4 - 1));
+            const int vv = qd / (RT * 4);
+            const int64_t at = (int64_t)vv * rows + min(tile0 * 16 + rl, rows - 4);
 #pragma unroll
-    for (int s = 1; s < kSkMaxSplits; s++)
-        if (s < n_splits) sum += t[s];
-    y[i] = sum;
+            for (int sl = 0; sl < kSkMaxSplits; sl++)
+                if (sl < n_splits) t[k][sl] = load_agent4(out + sl * split_stride + at);
+        }
+#pragma unroll
+        for (int k = 0; k < NQ; k++) {
+            const int qd = threadIdx.x + k * kSkWaves * 64;
+            const int rl = 4 * (qd & (RT * 4 - 1));
+            const int vv = qd / (RT * 4);
+            const int row = tile0 * 16 + rl;
+            floatx4 sum = t[k][0];
+#pragma unroll
+            for (int sl = 1; sl < kSkMaxSplits; sl++)
+                if (sl < n_splits) sum += t[k][sl];
+            if (row < rows && v0 + vv < n_vec) *reinterpret_cast<floatx4 *>(y + (int64_t)vv * rows + row) = sum;
+        }
+    } else {
+        for (int i = threadIdx.x; i < RT * 16 * NVT * 16; i += kSkWaves * 64) {
+            const int rl = i & (RT * 16 - 1);
+            const int vv = i / (RT * 16);
+            const int row = tile0 * 16 + rl;
+            if (row >= rows || v0 + vv >= n_vec) continue;
+            const int64_t at = (int64_t)vv * rows + row;
+            float sum = load_agent(out + at);
+            for (int sl = 1; sl < n_splits; sl++) sum += load_agent(out + sl * split_stride + at);
+            y[at] = sum;
+        }
+    }
 }
 
 template <int NVT>
 int launch_splitk(gla_ctx *ctx, const gla_q8w *w, const _Float16 *xp, const float *xs, int n_blocks_pad, int v0,
-                  int n_vec, int n_splits, float *out, int64_t split_stride) {
+                  int n_vec, int n_splits, float *out, int64_t split_stride, float *y, int32_t *arrivals) {
     const dim3 grid((w->n_tiles + kSkRT - 1) / kSkRT, n_splits);
     hipLaunchKernelGGL((matvec_q8_splitk_kernel<NVT>), grid, dim3(kSkWaves * 64), 0, ctx->stream, w->quants,
                        w->scales, w->rows, w->n_tiles, w->n_pairs, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out,
-                       split_stride);
+                       split_stride, y, arrivals);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "matvec_q8_splitk_kernel launch: %s", hipGetErrorString(e));
     return GLA_OK;
@@ -740,40 +799,39 @@ int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, f
     _Float16 *xp = (_Float16 *)scr;
     float *xs = (float *)((uint8_t *)scr + xp_bytes);
     float *part = (float *)((uint8_t *)scr + xp_bytes + xs_bytes);
-    const dim3 sgrid((n_blocks_pad * 4 + 256 * kSplitU - 1) / (256 * kSplitU), vec_pad);
+    const dim3 sgrid((n_blocks_pad * 4 + kSplitChunk - 1) / kSplitChunk, vec_pad / kSplitV);
     if (((uintptr_t)x & 15) == 0)  // rows start 128-byte apart: the base decides
-        hipLaunchKernelGGL(split_x_kernel<true>, sgrid, dim3(256), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad,
+        hipLaunchKernelGGL(split_x_kernel<true>, sgrid, dim3(kSplitThreads), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad,
                            xp, xs);
     else
-        hipLaunchKernelGGL(split_x_kernel<false>, sgrid, dim3(256), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad,
+        hipLaunchKernelGGL(split_x_kernel<false>, sgrid, dim3(kSplitThreads), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad,
                            xp, xs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "split_x_kernel launch: %s", hipGetErrorString(e));
+    // K slices summed in the split-K kernel by each row group's last workgroup
+    int32_t *arrivals = nullptr;
+    if (n_splits > 1) {
+        rc = ensure_arrivals(ctx, (size_t)n_groups, &arrivals);
+        if (rc != GLA_OK) return rc;
+    }
     for (int v0 = 0; v0 < n_vec; v0 += 16 * kMaxVT) {
         const int nvt = std::min(kMaxVT, (n_vec - v0 + 15) / 16);
         float *yv = y + (int64_t)v0 * w->rows;
         float *out = n_splits > 1 ? part : yv;
         switch (nvt) {
         case 1:
-            rc = launch_splitk<1>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride);
+            rc = launch_splitk<1>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv, arrivals);
             break;
         case 2:
-            rc = launch_splitk<2>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride);
+            rc = launch_splitk<2>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv, arrivals);
             break;
         case 3:
-            rc = launch_splitk<3>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride);
+            rc = launch_splitk<3>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv, arrivals);
             break;
         default:
-            rc = launch_splitk<4>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride);
+            rc = launch_splitk<4>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv, arrivals);
         }
         if (rc != GLA_OK) return rc;
-        if (n_splits > 1) {
-            const int64_t n_out = (int64_t)std::min(16 * kMaxVT, n_vec - v0) * w->rows;
-            hipLaunchKernelGGL(matvec_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, ctx->stream,
-                               part, n_splits, split_stride, n_out, yv);
-            e = hipGetLastError();
-            if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "matvec_reduce_kernel launch: %s", hipGetErrorString(e));
-        }
     }
     return GLA_OK;
 }
