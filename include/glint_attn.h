@@ -236,7 +236,9 @@ int gla_decode(gla_ctx *ctx, const gla_decode_args *args);
 #define GLA_DECODE_NOALLOC_SCRATCH_BYTES (16u << 20)
 /* (sequence, KV head, head group) units an f32-storage gla_decode_noalloc
  * call may hold (arrival counters of the short-window merge; one array per
- * GPU). */
+ * GPU). Never the tighter limit: a unit that counts arrivals has at least
+ * two split partials of at least 384 bytes each, so the partial scratch
+ * refuses a call before it reaches 21,846 such units. */
 #define GLA_DECODE_NOALLOC_UNITS 65536
 
 /* gla_decode that allocates nothing. It has no counterpart in the reference:
