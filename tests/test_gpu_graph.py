@@ -103,7 +103,8 @@ def test_graph_replays_equal_eager_calls(backend):
 
 def test_capture_that_would_grow_scratch_is_refused(backend):
     """A captured call whose scratch the stream has not yet sized is refused with
-    GLA_ERR_INVALID (an allocation is not allowed inside a capture); the stream works after."""
+    GLA_ERR_INVALID (an allocation is not allowed inside a capture); the stream works after, and
+    the captured 64-token matvec's replays equal eager calls on the same inputs bit for bit."""
     from glint_amd.attn import HipStream
     be = backend
     w = be.create_q8_weights(orc.q8_quantize_rows(synth.normal_rows(17, 256, 1024)).reshape(-1), 256, 1024)
@@ -116,10 +117,17 @@ def test_capture_that_would_grow_scratch_is_refused(backend):
         be.matvec_q8_0(w, x, 64, y)  # eager: sizes the stream's scratch
         be.sync()
         g = be.capture(lambda: be.matvec_q8_0(w, x, 64, y))
-        want = y.download((64 * 256,)).copy()
-        g.replay()
-        be.sync()
-        assert np.array_equal(y.download((64 * 256,)).view(np.uint32), want.view(np.uint32))
+        # replays with new inputs and eager calls between them: the split-K kernel's per-row-group
+        # arrival counters must be back at zero after every run for the next to sum its K slices
+        y2 = be.empty(64 * 256 * 4)
+        for rep in range(4):
+            x.upload(synth.normal_rows(19 + rep, 64, 1024))
+            be.matvec_q8_0(w, x, 64, y2)
+            g.replay()
+            be.sync()
+            want = y2.download((64 * 256,))
+            assert np.isfinite(want).all()
+            assert np.array_equal(y.download((64 * 256,)).view(np.uint32), want.view(np.uint32)), rep
         g.destroy()
     finally:
         be.set_stream(None)
