@@ -35,9 +35,17 @@ constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kStepsPerIter = 2;  // half-page token steps a lane group loads per iteration
-// Windows of at most this many pages merge their splits in the last
-// workgroup to finish instead of a combine launch.
-constexpr int kMergePages = 64;
+// A window of few splits merges them in the last of its workgroups to finish
+// instead of a combine launch. That workgroup's threads each merge
+// EPT = ceil(GT x D / 256) elements, reading their splits' partials in
+// batches of eight splits, one memory round trip per batch; the merge pays
+// for up to two batches, 16 splits of 4 pages. The bound is in pages and adds
+// the page a start inside a page brings (65 pages, a third batch of one
+// split), so a launch sized from max_kv_len = 1024 without host lengths needs
+// no combine. Above 2 elements per thread (a batch is 24 x EPT loads in flight
+// per thread) the bound is one batch, 33 pages.
+constexpr int merge_ept(int D, int gt) { return (gt * D + kThreads - 1) / kThreads; }
+constexpr int merge_max_pages(int D, int gt) { return merge_ept(D, gt) <= 2 ? 65 : 33; }
 
 struct DecodeParams {
     KvLayout kv;
@@ -57,10 +65,10 @@ struct DecodeParams {
     int max_len;  // host bound on kv_len: lengths are clamped to it, so splits never exceed max_splits
     float q_mul;    // multiplier of q.k: scale*log2(e), or scale with a soft-cap
     float softcap;  // > 0: cap * tanh(s / cap)
-    // Windows of at most merge_pages pages (and more than one split) are
-    // merged by the last of their workgroups to finish, counted in
-    // arrivals[unit] (0 between calls: the last arrival resets it); longer
-    // windows by decode_combine_kernel.
+    // Windows of more than one split and at most merge_pages pages are merged
+    // by the last of their workgroups to finish, counted in arrivals[unit] (0
+    // between calls: the last arrival resets it); longer windows by
+    // decode_combine_kernel.
     int merge_pages;
     int32_t *arrivals;
 };
@@ -167,40 +175,66 @@ __device__ __forceinline__ float word_f(const uint4 &c, int w) {
     return __uint_as_float(w == 0 ? c.x : (w == 1 ? c.y : (w == 2 ? c.z : c.w)));
 }
 
-// Merge of the splits of one unit's head g, element e, in split order, eight
-// splits at a time ((M, L, A) absorbing each batch with one rescale): the
-// last-arriving workgroup's merge of a short window.
+// The last-arriving workgroup's merge of a short window: thread tid merges
+// elements tid, tid + 256, ... (EPT of them) of the unit's gcount x D outputs,
+// in split order, eight splits at a time; each batch's loads for all of the
+// thread's elements are issued together (one memory round trip per batch), and
+// (M, L, A) absorb a batch with one rescale.
 template <int D, int GT>
-__device__ __forceinline__ float merge_splits_agent(const DecodeParams &p, int64_t slot0, int n_splits, int g, int e) {
-    float M = -INFINITY, L = 0.0f, A = 0.0f;
+__device__ __forceinline__ void merge_splits_agent(const DecodeParams &p, int64_t slot0, int n_splits, int gcount,
+                                                   float *out) {
+    constexpr int EPT = merge_ept(D, GT);
+    const int tid = threadIdx.x;
+    const int n_el = gcount * D;
+    int gk[EPT], ek[EPT];
+    float M[EPT], L[EPT], A[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; k++) {
+        const int idx = min(tid + k * kThreads, n_el - 1);
+        gk[k] = idx / D;
+        ek[k] = idx - gk[k] * D;
+        M[k] = -INFINITY;
+        L[k] = 0.0f;
+        A[k] = 0.0f;
+    }
     for (int s0 = 0; s0 < n_splits; s0 += 8) {
-        float mi[8], li[8], ai[8];
+        float mi[EPT][8], li[EPT][8], ai[EPT][8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int s = min(s0 + j, n_splits - 1);
-            mi[j] = load_agent(p.part_ml + (slot0 + s) * 32 + g);
-            li[j] = load_agent(p.part_ml + (slot0 + s) * 32 + 8 + g);
-            ai[j] = load_agent(p.part_acc + ((slot0 + s) * GT + g) * D + e);
-        }
-        const int nv = n_splits - s0;
-        float bm = M;
+        for (int k = 0; k < EPT; k++) {
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (j < nv) bm = fmaxf(bm, mi[j]);
-        const float f0 = (M == -INFINITY) ? 0.0f : fast_exp2(M - bm);
-        L *= f0;
-        A *= f0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (j < nv) {
-                const float f = (mi[j] == -INFINITY) ? 0.0f : fast_exp2(mi[j] - bm);
-                L = fmaf(li[j], f, L);
-                A = fmaf(ai[j], f, A);
+            for (int j = 0; j < 8; j++) {
+                const int64_t slot = slot0 + min(s0 + j, n_splits - 1);
+                mi[k][j] = load_agent(p.part_ml + slot * 32 + gk[k]);
+                li[k][j] = load_agent(p.part_ml + slot * 32 + 8 + gk[k]);
+                ai[k][j] = load_agent(p.part_acc + (slot * GT + gk[k]) * D + ek[k]);
             }
         }
-        M = bm;
+        const int nv = n_splits - s0;
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            float bm = M[k];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (j < nv) bm = fmaxf(bm, mi[k][j]);
+            const float f0 = (M[k] == -INFINITY) ? 0.0f : fast_exp2(M[k] - bm);
+            L[k] *= f0;
+            A[k] *= f0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (j < nv) {
+                    const float f = (mi[k][j] == -INFINITY) ? 0.0f : fast_exp2(mi[k][j] - bm);
+                    L[k] = fmaf(li[k][j], f, L[k]);
+                    A[k] = fmaf(ai[k][j], f, A[k]);
+                }
+            }
+            M[k] = bm;
+        }
     }
-    return L > 0.0f ? A * (1.0f / L) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < EPT; k++) {
+        const int idx = tid + k * kThreads;
+        if (idx < n_el) out[idx] = L[k] > 0.0f ? A[k] * (1.0f / L[k]) : 0.0f;
+    }
 }
 
 template <int D, int GT, int NSTEP, bool CAP>
@@ -455,12 +489,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
     // reached shared memory; the unit's last workgroup merges every split.
     __shared__ int lds_last;
     if (!arrive_last(p.arrivals + unit, r.n_splits, &lds_last)) return;
-    const int64_t slot0 = unit * p.max_splits;
-    for (int idx = tid; idx < gcount * D; idx += kThreads) {
-        const int g = idx / D;
-        const int e = idx - g * D;
-        p.out[((int64_t)b * p.n_heads + h_base + g) * D + e] = merge_splits_agent<D, GT>(p, slot0, r.n_splits, g, e);
-    }
+    merge_splits_agent<D, GT>(p, unit * p.max_splits, r.n_splits, gcount, p.out + ((int64_t)b * p.n_heads + h_base) * D);
 }
 
 // Log-sum-exp merge of the split partials of one (sequence, kv head, head
@@ -482,7 +511,7 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(const DecodePa
     const int gcount = min(GT, p.group - hg * GT);
     if (g >= gcount) return;
     const SeqRange r = seq_range(p, b);
-    if (r.n_splits <= 1 || r.n_pages <= p.merge_pages) return;  // (short windows merge in the split kernel)
+    if (r.n_splits <= 1 || r.n_pages <= p.merge_pages) return;  // (one split, or merged in the split kernel)
     const int sg = threadIdx.x / RL;
     const int e4 = threadIdx.x - sg * RL;
     const int64_t unit = ((int64_t)b * p.n_kv_heads + kvh) * p.n_hg + hg;
@@ -640,10 +669,10 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
     const bool cap = d.softcap > 0.0f;
     prm.q_mul = cap ? d.scale : d.scale * kLog2e;
     prm.softcap = cap ? d.softcap : 0.0f;
-    // Windows of up to kMergePages pages merge their splits in the split
-    // kernel's last workgroup (no combine launch); GLA_DECODE_MERGE_PAGES
-    // sets another bound (tuning only; 0: every window through the combine).
-    int merge_pages = kMergePages;
+    // Windows of up to merge_pages pages merge their splits in the split
+    // kernel's last workgroup (no combine launch); GLA_DECODE_MERGE_PAGES sets
+    // another bound (tuning only; 0: every window through the combine).
+    int merge_pages = merge_max_pages(D, gt);
     if (const char *env = getenv("GLA_DECODE_MERGE_PAGES")) merge_pages = std::max(0, atoi(env));
     prm.merge_pages = merge_pages;
     prm.arrivals = nullptr;
@@ -654,7 +683,7 @@ int launch_decode(gla_ctx *ctx, const DecodeLaunch &d) {
         for (int b = 0; b < d.n_seqs; b++) {
             const int n = host_seq_pages(d.kv_start_host[b], d.kv_len_host[b], d.max_kv_len, d.pm.pos_limit);
             const int pps = pps_fixed > 0 ? pps_fixed : split_pages(n);
-            if ((n + pps - 1) / pps <= 1) continue;
+            if (std::min((n + pps - 1) / pps, max_splits) <= 1) continue;
             if (n <= merge_pages)
                 any_short = true;
             else

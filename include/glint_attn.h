@@ -255,8 +255,8 @@ int gla_decode(gla_ctx *ctx, const gla_decode_args *args);
  * KV head against 5). Every call on one GPU shares that GPU's array: calls
  * that overlap on one GPU (two streams or two contexts) race. Nothing in it
  * needs clearing: a call writes every partial it reads. f32 windows of at
- * most 64 pages merge their splits in the last workgroup to finish and count
- * arrivals in a second static array of GLA_DECODE_NOALLOC_UNITS counters
+ * most 65 pages (33 at head groups of over 512 floats) merge their splits in
+ * the last workgroup to finish and count arrivals in a second static array of GLA_DECODE_NOALLOC_UNITS counters
  * (zero when the library loads, left at zero by every call); a call with
  * more (sequence, KV head, head group) units returns GLA_ERR_INVALID. */
 int gla_decode_noalloc(gla_ctx *ctx, const gla_decode_args *args);

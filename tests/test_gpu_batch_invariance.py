@@ -73,20 +73,22 @@ def test_decode_is_batch_invariant_cfg3(backend, cfg3_batch, dtype):
         pool.destroy()
 
 
-@pytest.mark.parametrize("d,h,hkv", [(64, 9, 3), (128, 32, 8)])
-def test_f32_merge_switch_is_batch_invariant(backend, d, h, hkv):
-    """f32 windows of up to 64 pages merge their splits in the split kernel's last workgroup to
-    arrive; longer ones in decode_combine_kernel. The choice is a rule on the window alone, so
-    windows on both sides of it (64 and 65 pages, from a page boundary and from mid-page, plus
-    one-split windows) give the same bits alone, in a batch that mixes both merges, in a shuffled
-    sub-batch and with the launch sized without host lengths; each matches the oracle, and the
-    arrival counters are left ready for the next call (a second run repeats the bits)."""
+@pytest.mark.parametrize("d,h,hkv,nb", [(64, 9, 3, 65), (128, 32, 8, 65)])
+def test_f32_merge_switch_is_batch_invariant(backend, d, h, hkv, nb):
+    """An f32 window of more than one split and at most nb = 65 pages (at these head shapes: 1
+    or 2 merged elements per thread) merges its splits in the split kernel's last workgroup to
+    arrive; longer ones in decode_combine_kernel. The choice is a rule on the window (and the model's head shape), so
+    windows on both sides of it (nb and nb + 1 pages, from a page boundary and from mid-page,
+    plus one-split windows) give the same bits alone, in a batch that mixes both merges, in a
+    shuffled sub-batch and with the launch sized without host lengths; each matches the oracle,
+    and the arrival counters are left ready for the next call (a second run repeats the bits)."""
     import oracle as orc
     from gpu_util import Contig
     from helpers import assert_close
 
     starts = np.array([0, 0, 0, 0, 0, 8, 8, 0, 5, 3], np.int32)
-    lens = np.array([1, 16, 17, 63 * 16, 64 * 16, 64 * 16 - 8, 64 * 16 - 7, 65 * 16, 2000, 130], np.int32)
+    lens = np.array([1, 16, 17, (nb - 1) * 16, nb * 16, nb * 16 - 8, nb * 16 - 7, (nb + 1) * 16, 2000, 130],
+                    np.int32)
     B = len(lens)
     c = Contig(backend, "f32", B, 1, int((starts + lens).max()), hkv, d, seed=5150 + d)
     q = synth.normal(5151 + d, (B, h, d))

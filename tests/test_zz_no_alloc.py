@@ -75,15 +75,16 @@ def test_noalloc_equals_decode_f32(backend):
 
 
 def test_noalloc_equals_decode_f32_mixed_windows(backend):
-    """A batch mixing f32 windows merged in the split kernel (at most 64 pages: the static arrival
-    counters) with ones merged by the combine kernel, then a smaller batch: bit for bit."""
-    H, Hkv, d = 9, 3, 64
+    """A batch mixing f32 windows merged in the split kernel (up to 65 pages: the static arrival
+    counters; here 300, 500 and 700 positions) with ones merged by the combine kernel (1050 and
+    2000), then a smaller batch of both kinds: bit for bit."""
+    H, Hkv, d = 32, 8, 128
     starts = np.array([0, 0, 5, 0, 0, 16, 3], np.int32)
-    lens = np.array([1, 17, 300, 1000, 1025, 2000, 700], np.int32)
+    lens = np.array([1, 17, 300, 500, 1050, 2000, 700], np.int32)
     c = Contig(backend, "f32", len(lens), 1, int((starts + lens).max()), Hkv, d, seed=9311)
-    for rows in (np.arange(len(lens)), np.array([1, 3, 6])):
+    for rows in (np.arange(len(lens)), np.array([1, 3, 5])):
         q = synth.normal(9312 + len(rows), (len(rows), H, d))
-        ref, got = _both(backend, c.cache, q, starts[rows], lens[rows], H, 0.125)
+        ref, got = _both(backend, c.cache, q, starts[rows], lens[rows], H, float(1 / np.sqrt(d)))
         assert np.array_equal(ref.view(np.uint32), got.view(np.uint32)), len(rows)
 
 
