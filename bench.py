@@ -562,6 +562,8 @@ def probe_lib():
     lib = C.CDLL(str(ROOT / "glint_amd" / "libglint_probe.so"))
     lib.glp_stream_read.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.POINTER(C.c_double)]
     lib.glp_mfma_peak.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double)]
+    lib.glp_read_per_launch.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_int, C.c_int,
+                                        C.POINTER(C.c_double)]
     return lib
 
 
@@ -593,9 +595,37 @@ class Settle:
         self.buf.free()
 
 
+# Per-launch read ceilings: the bytes one call of a small workload must read, read by one
+# launch of the streaming-read kernel (the best of these workgroup counts), launches back to
+# back over a 2 GiB buffer in rotation so that each comes from HBM. "empty" is the launch floor.
+PER_LAUNCH_READS = {
+    "empty": (16, (1,)),
+    "cfg1_call": (2 * 512 * 3 * 64 * 4, (64, 128, 256, 512)),         # K+V of one SmolLM layer, ctx 512
+    "proj_qkv_weights": (6144 * 128 * 34, (256, 512, 1024, 2048)),      # Q8_0 QKV weight bytes
+    "cfg2_layer": (2 * 4096 * 8 * 128 * 4, (256, 512, 1024, 2048, 4096)),  # K+V of one Llama layer, ctx 4096
+}
+
+
+def per_launch_reads(lib, buf, nbytes: int) -> dict:
+    out = {}
+    us = C.c_double()
+    for name, (size, grids) in PER_LAUNCH_READS.items():
+        best = None
+        for wgs in grids:
+            rc = lib.glp_read_per_launch(buf.ptr, nbytes, size, wgs, 200, C.byref(us))
+            if rc != 0:
+                raise RuntimeError(f"gla_probe glp_read_per_launch failed ({rc})")
+            if best is None or us.value < best[0]:
+                best = (us.value, wgs)
+        out[name] = {"bytes": size, "us": round(best[0], 2), "workgroups": best[1],
+                     "GB_per_s": round(size / (best[0] * 1e-6) / 1e9, 1)}
+    return out
+
+
 def achievable(be: GpuBackend, settle: Settle) -> dict:
     """Ceilings measured on this GPU (glint_amd/csrc/gla_probe.hip): a 2 GiB streaming read with
-    non-temporal loads, and MFMA-only loops for fp32 (16x16x4) and bf16 (16x16x32), each after a
+    non-temporal loads, one read per launch at the sizes of the small workloads
+    (PER_LAUNCH_READS), and MFMA-only loops for fp32 (16x16x4) and bf16 (16x16x32), each after a
     settle of its kind."""
     lib = settle.lib
     nbytes = 2 << 30
@@ -603,6 +633,7 @@ def achievable(be: GpuBackend, settle: Settle) -> dict:
     gbs, f32, bf16, bf16r, f32r = C.c_double(), C.c_double(), C.c_double(), C.c_double(), C.c_double()
     settle("hbm")
     rc = lib.glp_stream_read(buf.ptr, nbytes, 10, C.byref(gbs))
+    per_launch = per_launch_reads(lib, buf, nbytes) if rc == 0 else None
     if rc == 0:
         settle("mfma")
     for rc in (rc,
@@ -613,8 +644,10 @@ def achievable(be: GpuBackend, settle: Settle) -> dict:
     del buf
     return {"hbm_read_gbs": round(gbs.value, 1), "fp32_mfma_tflops": round(f32.value, 1),
             "bf16_mfma_tflops": round(bf16.value, 1), "bf16_mfma_random_data_tflops": round(bf16r.value, 1),
-            "fp32_mfma_random_data_tflops": round(f32r.value, 1),
-            "how": "2 GiB streaming read with non-temporal 16-byte loads; MFMA-only loops, 8 waves per CU, "
+            "fp32_mfma_random_data_tflops": round(f32r.value, 1), "read_per_launch": per_launch,
+            "how": "2 GiB streaming read with non-temporal 16-byte loads; one read per launch of each "
+                   "small workload's bytes, back to back over the 2 GiB buffer in rotation (best "
+                   "workgroup count; launch gaps included); MFMA-only loops, 8 waves per CU, "
                    "8 independent accumulators per wave, on near-constant operands and on random "
                    "N(0,1) operands (glint_amd/csrc/gla_probe.hip); each after a settle of its kind"}
 
@@ -734,6 +767,8 @@ def main() -> int:
             "value": round(gbs, 2), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2), "timing_us": t.summary_us(),
             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs"), "settle": settled}
+        if ach:
+            e["read_per_launch_ceiling_us"] = ach["read_per_launch"]["cfg2_layer"]["us"]
         defer(wl, lambda base, ref, errors, e=e: e.update(cpu_baseline=base, errors=errors))
         log(f"cfg2: {ms * 1e3:.1f} us/layer, {gbs:.1f} GB/s")
         del wl
@@ -747,6 +782,8 @@ def main() -> int:
             "workload": "SmolLM-135M decode, H9/KV3 d64, B=1, f32 contiguous ctx 512 (latency)",
             "value": round(ms * 1e3, 2), "unit": "us/call", "timing_us": t.summary_us(),
             "GB_per_s": round(wl.bytes_per_step() / (ms * 1e-3) / 1e9, 2), "settle": settled}
+        if ach:
+            e["read_per_launch_ceiling_us"] = ach["read_per_launch"]["cfg1_call"]["us"]
         log(f"cfg1: {ms * 1e3:.2f} us/call")
         # the same layers' calls captured as one HIP graph (a decode step's attention), replayed:
         # the launch cost of a call is then paid once per step, not once per kernel
@@ -819,6 +856,8 @@ def main() -> int:
                 "value": round(gbs, 2), "unit": "GB/s", "us_per_call": round(ms * 1e3, 2),
                 "timing_us": t.summary_us(), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                 "frac_of_achievable_hbm": frac_of(gbs, "hbm_read_gbs"), "settle": settled}
+            if ach:  # the weights alone, read by one launch
+                e["read_per_launch_ceiling_us"] = ach["read_per_launch"]["proj_qkv_weights"]["us"]
             def place_proj(base, ref, errors, e=e, n_vec=n_vec):
                 e["errors"] = errors
                 if n_vec == 1:

@@ -1,7 +1,9 @@
 // gla_probe.hip -- achievable-peak probes for the benchmark (not part of the
-// attention ABI): a streaming HBM read and MFMA-only loops, timed with HIP
-// events on the null stream. bench.py reports each kernel's throughput both
-// against MI355X's published peaks and against these measured ceilings.
+// attention ABI): a streaming HBM read (one pass over a large buffer, and one
+// chunk per launch for the per-launch ceilings of the small workloads) and
+// MFMA-only loops, timed with HIP events on the null stream. bench.py reports
+// each kernel's throughput both against MI355X's published peaks and against
+// these measured ceilings.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -178,6 +180,31 @@ int glp_stream_read(const void *buf, size_t bytes, int reps, double *gbs_out) {
     (void)hipFree(sink);
     if (rc != 0) return rc;
     *gbs_out = (double)bytes / (ms * 1e-3) / 1e9;
+    return 0;
+}
+
+// One read of `chunk` bytes per launch, back to back on the null stream,
+// each launch reading the next chunk of `bytes` in rotation (so that with
+// bytes past the 256 MB last-level cache every chunk comes from HBM), with
+// `wgs` workgroups of the streaming-read kernel; microseconds per launch,
+// launch gaps included. chunk and bytes are multiples of 16, chunk <= bytes.
+int glp_read_per_launch(const void *buf, size_t bytes, size_t chunk, int wgs, int reps, double *us_out) {
+    if (chunk == 0 || chunk % 16 != 0 || chunk > bytes || wgs <= 0 || reps <= 0) return -1;
+    uint32_t *sink = nullptr;
+    if (hipMalloc(&sink, 4) != hipSuccess) return -3;
+    const size_t n_chunks = bytes / chunk;
+    size_t next = 0;
+    float ms = 0.0f;
+    const int rc = time_ms(
+        [&] {
+            const u32x4 *a = reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(buf) + next * chunk);
+            next = (next + 1) % n_chunks;
+            hipLaunchKernelGGL(stream_read_kernel, dim3(wgs), dim3(256), 0, nullptr, a, chunk / 16, sink);
+        },
+        reps, &ms);
+    (void)hipFree(sink);
+    if (rc != 0) return rc;
+    *us_out = (double)ms * 1e3;
     return 0;
 }
 
