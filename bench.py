@@ -301,7 +301,7 @@ class PagedDecode:
     def bytes_per_step(self):
         return float(np.mean([L["bytes"] for L in self.layers]))
 
-    def cpu_baseline(self, cb: CpuBaseline, min_seconds=10.0, max_reps=50):
+    def cpu_baseline(self, cb: CpuBaseline, min_seconds=10.0, max_reps=200):
         """Layer 0 of every sequence through the oracle's decode_batch, one task per sequence.
         Returns (baseline, the oracle's output [B][H][d])."""
         orc = cb.orc
