@@ -9,8 +9,11 @@ writes (cache/mod.rs:296-315) over shapes, scales and special values, and the ho
 attention entry points (backend/gpu.rs:266-397, :860-992). Every case
 is drawn from its own fixed seed, so a failure names a reproducible
 shape. Bars: fp32 abs 1e-4 / rel 1e-3; bf16-input prefill abs 3e-2 / rel 3e-2 against the fp32
-oracle (helpers.py), and bit-identical to the per-workgroup bf16 path."""
+oracle (helpers.py), and bit-identical to the per-workgroup bf16 path. GLA_TEST_SWEEP=k runs k
+times as many cases of every family (the first ones are always the same; the default is 1)."""
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -22,9 +25,10 @@ from helpers import BF16_ABS_TOL, BF16_REL_TOL, assert_close
 
 pytestmark = pytest.mark.gpu
 
-N_PREFILL = 32
-N_DECODE = 32
-N_PAGED = 16
+SWEEP = max(1, int(os.environ.get("GLA_TEST_SWEEP", "1")))
+N_PREFILL = 32 * SWEEP
+N_DECODE = 32 * SWEEP
+N_PAGED = 16 * SWEEP
 
 
 def _prefill_case(i):
@@ -166,7 +170,7 @@ def test_paged_random_shapes(backend, case):
         assert_close(got[rows], want, *tol, what=f"case {case} {c_} prefill seq {b}")
 
 
-N_MATVEC = 24
+N_MATVEC = 24 * SWEEP
 
 
 def _matvec_case(i):
@@ -216,7 +220,7 @@ def test_matvec_random_shapes(backend, case):
         assert np.all(np.abs(got[v] - want) <= 4e-6 * mag[v]), (case, c_, v)
 
 
-N_ROPE = 16
+N_ROPE = 16 * SWEEP
 
 
 @pytest.mark.parametrize("case", range(N_ROPE))
@@ -248,7 +252,7 @@ def test_rope_random_shapes(backend, case):
     assert np.array_equal(got[0], x[0]), case   # position 0 is the identity
 
 
-N_KV_WRITE = 16
+N_KV_WRITE = 16 * SWEEP
 
 
 @pytest.mark.parametrize("case", range(N_KV_WRITE))
@@ -304,7 +308,7 @@ def test_kv_write_random_shapes(backend, case):
     pool.destroy()
 
 
-N_HOST_ATTN = 16
+N_HOST_ATTN = 16 * SWEEP
 
 
 @pytest.mark.parametrize("case", range(N_HOST_ATTN))
@@ -343,7 +347,7 @@ def test_host_attention_random_shapes(backend, case):
                  what=f"case {case} resident {dtype} d {d} H {H}/{hkv} seq {seq} layer {layer} [{start}, +{attend})")
 
 
-N_ODD_GROUPS = 12
+N_ODD_GROUPS = 12 * SWEEP
 
 
 @pytest.mark.parametrize("case", range(N_ODD_GROUPS))
@@ -376,7 +380,7 @@ def test_decode_odd_groups_random(backend, case):
     assert_close(got, want.reshape(B, H, d), what=f"case {case} d {d} H {H}/{hkv} {dtype} B {B}")
 
 
-N_PREFILL_ODD = 10
+N_PREFILL_ODD = 10 * SWEEP
 
 
 @pytest.mark.parametrize("case", range(N_PREFILL_ODD))
