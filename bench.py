@@ -30,7 +30,8 @@ bench runs a different kernel of the leg's kind -- ~0.1 s of streaming reads
 of a 1 GiB buffer for the HBM-bound legs, ~0.3 s of the bf16 MFMA loop on
 random operands for the prefill legs (glint_amd/csrc/gla_probe.hip) -- and
 the timed steps measure what the path sustains. The W warmup and K timed steps are the leg's own, unchanged;
-"settle" in the JSON says what ran.
+"settle" in the JSON says what ran. --no-settle leaves it out (to measure its effect,
+profiles/settle_effect.md).
 
 roofline: algorithmic bytes of one call (unique K/V bytes of the attended
 positions, page-table entries, q and out) divided by the call's median
@@ -577,11 +578,14 @@ class Settle:
     HOW = {"hbm": "625 streaming reads of a 1 GiB buffer (glp_stream_read), ~0.1 s",
            "mfma": "bf16 MFMA-only loop on random operands, 550,000 iterations (glp_mfma_peak mode 2), ~0.3 s"}
 
-    def __init__(self, be: GpuBackend):
+    def __init__(self, be: GpuBackend, on: bool = True):
         self.lib = probe_lib()
         self.buf = be.empty(1 << 30)
+        self.on = on
 
     def __call__(self, kind: str) -> str:
+        if not self.on:
+            return "none"
         out = C.c_double()
         if kind == "hbm":
             rc = self.lib.glp_stream_read(self.buf.ptr, 1 << 30, 625, C.byref(out))
@@ -662,6 +666,8 @@ def main() -> int:
     ap.add_argument("--calibrate", action="store_true", help="also run known-size page copies (for PMC runs)")
     ap.add_argument("--achievable", action="store_true",
                     help="measure the achievable ceilings also when one workload is selected")
+    ap.add_argument("--no-settle", action="store_true",
+                    help="no settle kernel before each leg's warmup (to measure the settle's effect)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU: the attention path has no multi-GPU leg "
@@ -682,8 +688,9 @@ def main() -> int:
     }
     secondary = {}
     ach = None
-    settle = Settle(be)
-    result["settle"] = {"before": "each leg's warmup, after its set-up", **Settle.HOW}
+    settle = Settle(be, on=not args.no_settle)
+    result["settle"] = ({"before": "each leg's warmup, after its set-up", **Settle.HOW} if settle.on
+                        else {"before": "none (--no-settle)"})
     if args.workload == "all" or args.achievable:
         log("achievable ceilings (streaming read, MFMA loops)")
         ach = achievable(be, settle)
