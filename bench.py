@@ -565,6 +565,7 @@ def probe_lib():
     lib.glp_mfma_peak.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double)]
     lib.glp_read_per_launch.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_int, C.c_int,
                                         C.POINTER(C.c_double)]
+    lib.glp_mfma_clock.argtypes = [C.c_int, C.POINTER(C.c_double)]
     return lib
 
 
@@ -640,20 +641,24 @@ def achievable(be: GpuBackend, settle: Settle) -> dict:
     per_launch = per_launch_reads(lib, buf, nbytes) if rc == 0 else None
     if rc == 0:
         settle("mfma")
+    mhz = C.c_double()
     for rc in (rc,
                lib.glp_mfma_peak(0, 50000, C.byref(f32)), lib.glp_mfma_peak(1, 50000, C.byref(bf16)),
-               lib.glp_mfma_peak(2, 50000, C.byref(bf16r)), lib.glp_mfma_peak(3, 50000, C.byref(f32r))):
+               lib.glp_mfma_peak(2, 50000, C.byref(bf16r)), lib.glp_mfma_peak(3, 50000, C.byref(f32r)),
+               lib.glp_mfma_clock(200000, C.byref(mhz))):
         if rc != 0:
             raise RuntimeError(f"gla_probe call failed ({rc})")
     del buf
     return {"hbm_read_gbs": round(gbs.value, 1), "fp32_mfma_tflops": round(f32.value, 1),
             "bf16_mfma_tflops": round(bf16.value, 1), "bf16_mfma_random_data_tflops": round(bf16r.value, 1),
-            "fp32_mfma_random_data_tflops": round(f32r.value, 1), "read_per_launch": per_launch,
+            "fp32_mfma_random_data_tflops": round(f32r.value, 1),
+            "bf16_mfma_random_data_clock_mhz": round(mhz.value), "read_per_launch": per_launch,
             "how": "2 GiB streaming read with non-temporal 16-byte loads; one read per launch of each "
                    "small workload's bytes, back to back over the 2 GiB buffer in rotation (best "
                    "workgroup count; launch gaps included); MFMA-only loops, 8 waves per CU, "
                    "8 independent accumulators per wave, on near-constant operands and on random "
-                   "N(0,1) operands (glint_amd/csrc/gla_probe.hip); each after a settle of its kind"}
+                   "N(0,1) operands, and the shader clock the random-operand bf16 loop runs at "
+                   "(glint_amd/csrc/gla_probe.hip); each after a settle of its kind"}
 
 
 def main() -> int:

@@ -71,7 +71,9 @@ __global__ __launch_bounds__(256) void mfma_bf16_kernel(int iters, float *sink) 
 // turn. The matrix units draw more power multiplying such data than the
 // near-constant operands above, and the part lowers its clock for it, so this
 // is the ceiling for attention on real activations.
-__global__ __launch_bounds__(256) void mfma_bf16_rand_kernel(int iters, float *sink) {
+// clk (when not null): workgroup 0's shader-clock count (s_memtime) and
+// 100 MHz real-time count (s_memrealtime) at the start and the end of its loop.
+__global__ __launch_bounds__(256) void mfma_bf16_rand_kernel(int iters, float *sink, unsigned long long *clk) {
     floatx4 c[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) c[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -95,6 +97,7 @@ __global__ __launch_bounds__(256) void mfma_bf16_rand_kernel(int iters, float *s
             a[r][k] = (__bf16)x[0];
             b[r][k] = (__bf16)x[1];
         }
+    const unsigned long long c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
     for (int it = 0; it < iters; it++)
 #pragma unroll
         for (int j = 0; j < 8; j++)
@@ -103,6 +106,13 @@ __global__ __launch_bounds__(256) void mfma_bf16_rand_kernel(int iters, float *s
 #pragma unroll
     for (int j = 0; j < 8; j++) s += c[j][0] + c[j][1] + c[j][2] + c[j][3];
     if (s == 12345.0f) sink[0] = s;
+    if (clk && blockIdx.x == 0 && threadIdx.x == 0) {
+        const unsigned long long c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+        clk[0] = c0;
+        clk[1] = c1;
+        clk[2] = r0;
+        clk[3] = r1;
+    }
 }
 
 // The fp32 loop on random N(0, 1) operands (as mfma_bf16_rand_kernel).
@@ -230,8 +240,8 @@ int glp_mfma_peak(int kind, int iters, double *tflops_out) {
         rc = time_ms([&] { hipLaunchKernelGGL(mfma_bf16_kernel, grid, block, 0, nullptr, iters, sink); }, 3, &ms);
         flops_per_mfma = 16.0 * 16 * 32 * 2;
     } else if (kind == 2) {
-        rc = time_ms([&] { hipLaunchKernelGGL(mfma_bf16_rand_kernel, grid, block, 0, nullptr, iters, sink); }, 3,
-                     &ms);
+        rc = time_ms([&] { hipLaunchKernelGGL(mfma_bf16_rand_kernel, grid, block, 0, nullptr, iters, sink, nullptr); },
+                     3, &ms);
         flops_per_mfma = 16.0 * 16 * 32 * 2;
     } else {
         rc = time_ms([&] { hipLaunchKernelGGL(mfma_f32_rand_kernel, grid, block, 0, nullptr, iters, sink); }, 3,
@@ -242,6 +252,37 @@ int glp_mfma_peak(int kind, int iters, double *tflops_out) {
     if (rc != 0) return rc;
     const double waves = (double)grid.x * 4;
     *tflops_out = waves * iters * 8 * flops_per_mfma / (ms * 1e-3) / 1e12;
+    return 0;
+}
+
+// The shader clock the bf16 MFMA loop on random operands runs at (MHz, from
+// workgroup 0's s_memtime and s_memrealtime over its loop, one launch after a
+// warm-up launch): the matrix units draw more power on random data and the
+// part lowers its clock to hold it.
+int glp_mfma_clock(int iters, double *mhz_out) {
+    unsigned long long *clk = nullptr;
+    float *sink = nullptr;
+    if (hipMalloc(&clk, 4 * sizeof(unsigned long long)) != hipSuccess) return -3;
+    if (hipMalloc(&sink, 4) != hipSuccess) {
+        (void)hipFree(clk);
+        return -3;
+    }
+    int n_cu = 0;
+    int rc = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess || n_cu <= 0) rc = -3;
+    unsigned long long h[4] = {0, 0, 0, 0};
+    if (rc == 0) {
+        for (int i = 0; i < 2; i++)
+            hipLaunchKernelGGL(mfma_bf16_rand_kernel, dim3(n_cu * 2), dim3(256), 0, nullptr, iters, sink, clk);
+        if (hipDeviceSynchronize() != hipSuccess || hipGetLastError() != hipSuccess ||
+            hipMemcpy(h, clk, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess)
+            rc = -4;
+    }
+    (void)hipFree(clk);
+    (void)hipFree(sink);
+    if (rc != 0) return rc;
+    if (h[3] <= h[2]) return -4;
+    *mhz_out = (double)(h[1] - h[0]) / ((double)(h[3] - h[2]) / 100.0);
     return 0;
 }
 
