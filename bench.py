@@ -644,8 +644,8 @@ def achievable(be: GpuBackend, settle: Settle) -> dict:
     mhz = C.c_double()
     for rc in (rc,
                lib.glp_mfma_peak(0, 50000, C.byref(f32)), lib.glp_mfma_peak(1, 50000, C.byref(bf16)),
-               lib.glp_mfma_peak(2, 50000, C.byref(bf16r)), lib.glp_mfma_peak(3, 50000, C.byref(f32r)),
-               lib.glp_mfma_clock(200000, C.byref(mhz))):
+               lib.glp_mfma_peak(2, 50000, C.byref(bf16r)), lib.glp_mfma_clock(50000, C.byref(mhz)),
+               lib.glp_mfma_peak(3, 50000, C.byref(f32r))):
         if rc != 0:
             raise RuntimeError(f"gla_probe call failed ({rc})")
     del buf
