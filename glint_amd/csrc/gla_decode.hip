@@ -105,6 +105,19 @@ __device__ __forceinline__ float max32(float x) {
     const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
 }
+// Two values' row-pair sums with one swap: rows 0 and 2 of the result hold
+// x's r0 + r1 and r2 + r3, rows 1 and 3 y's (v_permlane16_swap exchanges
+// rows 1, 3 of x with rows 0, 2 of y).
+__device__ __forceinline__ float pair16(float x, float y) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+// Two pair16 results s (of x, y) and t (of z, w) summed across the halves:
+// row 0 holds x's total, row 1 y's, row 2 z's, row 3 w's.
+__device__ __forceinline__ float pair32(float s, float t) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(t), false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
 
 // tanh(x) = sign(x) (1 - t) / (1 + t), t = exp(-2|x|).
 __device__ __forceinline__ float tanh_approx(float x) {
@@ -394,34 +407,41 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
     }
 
     // merge the 8 lane groups of the wave (lanes with equal `sub` own the
-    // same elements)
+    // same elements): the maxima and sums of each head as all-reductions,
+    // the GT x EPL output sums as a reduce-scatter over the same tree
+    // (lane ^ 8, then ^ 16, then ^ 32) with two values per row swap: after
+    // it, row r of the wave holds value 4k + r of each group of four, and
+    // the row's first 8 lanes write it. The first step is written as the
+    // fused multiply-add it compiles to, so that every value rounds alike
+    // (left to the compiler, the contraction differs between values).
 #pragma unroll
     for (int g = 0; g < GT; g++) {
         float M = m[g];
         M = max32(max16(fmaxf(M, other8(M))));
         const float f = (m[g] == -INFINITY) ? 0.0f : fast_exp2(m[g] - M);
-        float lg = l[g] * f;
-        lg = add32(add16(lg + other8(lg)));
+        float lg = fmaf(l[g], f, other8(l[g] * f));
+        lg = add32(add16(lg));
 #pragma unroll
-        for (int e = 0; e < EPL; e++) {
-            float a = acc[g][e] * f;
-            a = add32(add16(a + other8(a)));
-            acc[g][e] = a;
-        }
+        for (int e = 0; e < EPL; e++) acc[g][e] = fmaf(acc[g][e], f, other8(acc[g][e] * f));
         m[g] = M;
         l[g] = lg;
     }
-    if (lane < 8) {
+    static_assert(EPL % 4 == 0, "groups of four values");
+    const int row = lane >> 4;
+#pragma unroll
+    for (int k = 0; k < GT * EPL / 4; k++) {
+        const int g = (4 * k) / EPL, j = (4 * k) % EPL;  // the group's first value: head g, element slot j
+        const float u = pair32(pair16(acc[g][j], acc[g][j + 1]), pair16(acc[g][j + 2], acc[g][j + 3]));
+        if ((lane & 8) == 0) {
+            const int jr = j + row;  // this row's value: element slot jr of head g
+            lds_acc[wave][g][((jr / EPC) * 8 + sub) * EPC + jr % EPC] = u;
+        }
+    }
+    if (lane == 0) {
 #pragma unroll
         for (int g = 0; g < GT; g++) {
-#pragma unroll
-            for (int i = 0; i < NCH; i++)
-#pragma unroll
-                for (int e = 0; e < EPC; e++) lds_acc[wave][g][(i * 8 + sub) * EPC + e] = acc[g][i * EPC + e];
-            if (lane == 0) {
-                lds_m[wave][g] = m[g];
-                lds_l[wave][g] = l[g];
-            }
+            lds_m[wave][g] = m[g];
+            lds_l[wave][g] = l[g];
         }
     }
     __syncthreads();
