@@ -15,13 +15,14 @@
 // (l/16)*8 .. +8 of each block, stored as x + 128 so that one v_perm makes
 // the exact f16 of 1024 + byte), and the pair's 32 scales are one 16-byte
 // read per lane. The activations are split per call into two f16 pieces
-// (hi = f16(x * 2^s), lo = f16(x * 2^s - hi), s per vector putting the
-// largest |x| near 2^14), so each block's product runs as two MFMAs with
+// (hi = f16(x * 2^s), lo = f16(x * 2^s - hi), s per vector and K slice
+// putting the slice's largest |x| near 2^14), so each block's product runs as two MFMAs with
 // exact int8 x f16 products and f32 accumulation; the f16 block scale is
 // applied in f32 per block, as the reference applies it. Each launch covers
 // up to 64 vectors, so the weights are read once per 64 vectors; K is split
-// across workgroups (the slices summed in order by a second kernel) so that
-// each CU reads only its slice of the activation pieces. Up to four vectors
+// across workgroups (the slices summed in order by each row group's last
+// workgroup to finish) so that each CU reads only its slice of the
+// activation pieces. Up to four vectors
 // take the vector-ALU kernel instead (x in f32 from LDS, no pieces). Bound:
 // HBM on the weights (34 bytes per 32 weights).
 #include <hip/hip_runtime.h>
@@ -143,56 +144,66 @@ __global__ __launch_bounds__(256) void q8w_repack_kernel(const uint8_t *ggml, in
 
 // ---- activations: f16 pieces ---------------------------------------------------
 
-// Grid (chunks of kSplitChunk units, padded vector count / 4), 1024 threads:
-// a workgroup takes 4 consecutive vectors (thread t always vector t & 3) and
-// the units of its chunk, kSplitU per thread; vectors past n_vec get zero pieces. Each thread
-// holds its units' 8 elements each in registers; a vector's largest |x|
-// comes from those registers when one chunk covers the vector (a second,
-// streaming read otherwise), and the pieces are written from the same
-// registers, in the B-operand order of the MFMA: xp[v / 16][blk][piece][lane
-// = kg*16 + v % 16] = 8 f16 of elements blk*32 + kg*8 .. +8 (piece 0 hi, 1
-// lo), so that one vector tile's piece of a block is 1 KiB contiguous; xs[v]
-// = 2^-s, the factor that undoes the scaling. With 4 vectors per workgroup,
-// 4 consecutive lanes write 4 consecutive 16-byte pieces, one 64-byte
-// request (one vector per workgroup wrote each piece as a 32-byte request).
-constexpr int kSplitThreads = 1024;
-constexpr int kSplitU = 2;                                      // units per thread
-constexpr int kSplitV = 4;                                      // vectors per workgroup
-constexpr int kSplitStep = kSplitThreads / kSplitV;             // units of a vector per pass
-constexpr int kSplitChunk = kSplitU * kSplitStep;               // units per workgroup
+// Grid (K slices of the split-K kernel, padded vector count / 4), 256
+// threads: a workgroup takes 4 consecutive vectors (thread t always vector
+// t & 3) and the units (8 elements each) of one K slice, block pairs
+// slice*ps .. +ps. Each (vector, slice) takes its own piece scale 2^s from
+// the slice's largest |x| alone, so no workgroup waits for another, and the
+// split-K kernel undoes it where it already multiplies a slice's sums by
+// one factor per vector. Up to kSplitU units per thread stay in registers
+// between the maximum and the pieces; a wider slice is read twice. Vectors
+// past n_vec get zero pieces. The pieces go out in the B-operand order of
+// the MFMA: xp[v / 16][blk][piece][lane = kg*16 + v % 16] = 8 f16 of
+// elements blk*32 + kg*8 .. +8 (piece 0 hi, 1 lo), so that one vector
+// tile's piece of a block is 1 KiB contiguous and 4 consecutive lanes write
+// 4 consecutive 16-byte pieces, one 64-byte request; xs[slice][v] = 2^-s,
+// the factor that undoes the scaling.
+constexpr int kSplitThreads = 256;
+constexpr int kSplitV = 4;                           // vectors per workgroup
+constexpr int kSplitStep = kSplitThreads / kSplitV;  // units of a vector per pass
+constexpr int kSplitU = 4;                           // units per thread held in registers
 template <bool A16>  // x rows 16-byte aligned: float4 loads
 __global__ __launch_bounds__(kSplitThreads) void split_x_kernel(const float *x, int n_vec, int cols,
-                                                                int n_blocks_pad, _Float16 *xp, float *xs) {
+                                                                int n_blocks_pad, int ps, int vec_pad,
+                                                                _Float16 *xp, float *xs) {
     const int vq = threadIdx.x & (kSplitV - 1);
     const int v = blockIdx.y * kSplitV + vq;
     const float *xv = x + (int64_t)min(v, n_vec - 1) * cols;
-    const int n_units = n_blocks_pad * 4;
-    const int cu = cols / 8;  // units inside the row (cols is a multiple of 32)
-    const int ut = threadIdx.x / kSplitV;  // the thread's unit within each pass
+    const int cu = cols / 8;                               // units inside the row (cols is a multiple of 32)
+    const int u0 = blockIdx.x * ps * 8;                    // the slice's units: 8 per block pair
+    const int u1 = min(n_blocks_pad * 4, u0 + ps * 8);
+    const int uin = min(u1, cu);                           // units of the slice inside the row
+    const int ut = threadIdx.x / kSplitV;                  // the thread's unit within each pass
+    // units past the slice (or the row) are zeros and load nothing: a
+    // clamped load there would read other slices' lines again
+    auto load_unit = [&](float (&e)[8], int u) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) e[j] = 0.0f;
+        if (v >= n_vec || u >= uin) return;
+        const float *src = xv + (int64_t)u * 8;
+        if (A16) {
+            const float4 a = *reinterpret_cast<const float4 *>(src);
+            const float4 b = *reinterpret_cast<const float4 *>(src + 4);
+            e[0] = a.x, e[1] = a.y, e[2] = a.z, e[3] = a.w;
+            e[4] = b.x, e[5] = b.y, e[6] = b.z, e[7] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) e[j] = src[j];
+        }
+    };
     float e[kSplitU][8];
     float mx = 0.0f;
 #pragma unroll
     for (int k = 0; k < kSplitU; k++) {
-        const int u = blockIdx.x * kSplitChunk + k * kSplitStep + ut;
-        const float *src = xv + (int64_t)min(u, cu - 1) * 8;  // clamped: loads stay in the row
-        if (A16) {
-            const float4 a = *reinterpret_cast<const float4 *>(src);
-            const float4 b = *reinterpret_cast<const float4 *>(src + 4);
-            e[k][0] = a.x, e[k][1] = a.y, e[k][2] = a.z, e[k][3] = a.w;
-            e[k][4] = b.x, e[k][5] = b.y, e[k][6] = b.z, e[k][7] = b.w;
-        } else {
+        load_unit(e[k], u0 + k * kSplitStep + ut);
 #pragma unroll
-            for (int j = 0; j < 8; j++) e[k][j] = src[j];
-        }
-        const bool in = v < n_vec && u < cu;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            e[k][j] = in ? e[k][j] : 0.0f;
-            mx = fmaxf(mx, fabsf(e[k][j]));
-        }
+        for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(e[k][j]));
     }
-    if (gridDim.x > 1 && v < n_vec) {  // rows wider than one chunk: the rest of the row's maximum
-        for (int c = ut; c < cols; c += kSplitStep) mx = fmaxf(mx, fabsf(xv[c]));
+    for (int u = u0 + kSplitU * kSplitStep + ut; u < uin; u += kSplitStep) {  // the rest of a wide slice
+        float t[8];
+        load_unit(t, u);
+#pragma unroll
+        for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(t[j]));
     }
     // maximum over the threads of the same vector: lanes of equal t & 3 in
     // the wave, then the waves
@@ -208,15 +219,12 @@ __global__ __launch_bounds__(kSplitThreads) void split_x_kernel(const float *x, 
     if (mx > 0.0f && isfinite(mx)) frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
     const int sh = 14 - ex;                            // the largest |x| * 2^sh lies in [2^13, 2^14)
     const float mul = ldexpf(1.0f, sh);
-    if (blockIdx.x == 0 && threadIdx.x < kSplitV) xs[v] = ldexpf(1.0f, -sh);
-#pragma unroll
-    for (int k = 0; k < kSplitU; k++) {
-        const int u = blockIdx.x * kSplitChunk + k * kSplitStep + ut;
-        if (u >= n_units) break;
+    if (threadIdx.x < kSplitV) xs[(int64_t)blockIdx.x * vec_pad + v] = ldexpf(1.0f, -sh);
+    auto put = [&](const float (&t8)[8], int u) {
         half8 hi, lo;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float t = e[k][j] * mul;
+            const float t = t8[j] * mul;
             const _Float16 h = (_Float16)t;
             hi[j] = h;
             lo[j] = (_Float16)(t - (float)h);
@@ -226,6 +234,16 @@ __global__ __launch_bounds__(kSplitThreads) void split_x_kernel(const float *x, 
         _Float16 *dst = xp + (((int64_t)(v >> 4) * n_blocks_pad + blk) * 128 + ln) * 8;
         *reinterpret_cast<half8 *>(dst) = hi;
         *reinterpret_cast<half8 *>(dst + 64 * 8) = lo;
+    };
+#pragma unroll
+    for (int k = 0; k < kSplitU; k++) {
+        const int u = u0 + k * kSplitStep + ut;
+        if (u < u1) put(e[k], u);
+    }
+    for (int u = u0 + kSplitU * kSplitStep + ut; u < u1; u += kSplitStep) {
+        float t[8];
+        load_unit(t, u);
+        put(t, u);
     }
 }
 
@@ -266,7 +284,7 @@ constexpr int kSkTargetWgs = 512;
 // wave holds 4 row tiles x NVT vector tiles of accumulators, so every x
 // fragment it loads serves four row tiles and every weight fragment NVT
 // vector tiles. The waves are merged in LDS in a fixed order and the slice's
-// sums (times the vector's piece factor) go to out[s][vv][row] as agent-scope
+// sums (times the piece factor of the vector in this slice) go to out[s][vv][row] as agent-scope
 // stores, or straight to y when there is one slice; the row group's last
 // workgroup to arrive (counted in arrivals[row group]) sums the slices into
 // y, so no reduce launch follows. Splitting K across workgroups is what keeps
@@ -274,8 +292,8 @@ constexpr int kSkTargetWgs = 512;
 template <int NVT>
 __global__ __launch_bounds__(kSkWaves * 64) void matvec_q8_splitk_kernel(
     const uint8_t *quants, const uint16_t *scales, int rows, int n_tiles, int n_pairs, const _Float16 *xp,
-    const float *xs, int n_blocks_pad, int v0, int n_vec, int n_splits, float *out, int64_t split_stride, float *y,
-    int32_t *arrivals) {
+    const float *xs, int xs_stride, int n_blocks_pad, int v0, int n_vec, int n_splits, float *out,
+    int64_t split_stride, float *y, int32_t *arrivals) {
     constexpr int RT = kSkRT;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -288,8 +306,8 @@ __global__ __launch_bounds__(kSkWaves * 64) void matvec_q8_splitk_kernel(
     const int p0 = min(q1, q0 + wave * per);
     const int p1 = min(q1, p0 + per);
 
-    __shared__ float xsl[NVT * 16];  // the launch's piece factors, read by the epilogue
-    if ((int)threadIdx.x < NVT * 16) xsl[threadIdx.x] = xs[v0 + threadIdx.x];
+    __shared__ float xsl[NVT * 16];  // this slice's piece factors of the launch's vectors, read by the epilogue
+    if ((int)threadIdx.x < NVT * 16) xsl[threadIdx.x] = xs[(int64_t)blockIdx.y * xs_stride + v0 + threadIdx.x];
 
     floatx4 acc[RT][NVT];
 #pragma unroll
@@ -450,12 +468,13 @@ __global__ __launch_bounds__(kSkWaves * 64) void matvec_q8_splitk_kernel(
 }
 
 template <int NVT>
-int launch_splitk(gla_ctx *ctx, const gla_q8w *w, const _Float16 *xp, const float *xs, int n_blocks_pad, int v0,
-                  int n_vec, int n_splits, float *out, int64_t split_stride, float *y, int32_t *arrivals) {
+int launch_splitk(gla_ctx *ctx, const gla_q8w *w, const _Float16 *xp, const float *xs, int xs_stride,
+                  int n_blocks_pad, int v0, int n_vec, int n_splits, float *out, int64_t split_stride, float *y,
+                  int32_t *arrivals) {
     const dim3 grid((w->n_tiles + kSkRT - 1) / kSkRT, n_splits);
     hipLaunchKernelGGL((matvec_q8_splitk_kernel<NVT>), grid, dim3(kSkWaves * 64), 0, ctx->stream, w->quants,
-                       w->scales, w->rows, w->n_tiles, w->n_pairs, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out,
-                       split_stride, y, arrivals);
+                       w->scales, w->rows, w->n_tiles, w->n_pairs, xp, xs, xs_stride, n_blocks_pad, v0, n_vec,
+                       n_splits, out, split_stride, y, arrivals);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "matvec_q8_splitk_kernel launch: %s", hipGetErrorString(e));
     return GLA_OK;
@@ -790,7 +809,8 @@ int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, f
     const int n_splits = std::max(1, std::min({kSkMaxSplits, (kSkTargetWgs + n_groups / 2) / n_groups,
                                                w->n_pairs / kSkWaves}));
     const size_t xp_bytes = (size_t)vec_pad * n_blocks_pad * 32 * 2 * sizeof(_Float16);  // hi + lo per element
-    const size_t xs_bytes = ((size_t)vec_pad * sizeof(float) + 255) / 256 * 256;
+    const int ps = (w->n_pairs + n_splits - 1) / n_splits;  // block pairs per slice, as the split-K kernel takes them
+    const size_t xs_bytes = ((size_t)n_splits * vec_pad * sizeof(float) + 255) / 256 * 256;  // [slice][vector]
     const int64_t split_stride = (int64_t)16 * kMaxVT * w->rows;  // one slice of partials: 64 vectors x rows
     const size_t part_bytes = n_splits > 1 ? (size_t)n_splits * split_stride * sizeof(float) : 0;
     void *scr = nullptr;
@@ -799,13 +819,13 @@ int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, f
     _Float16 *xp = (_Float16 *)scr;
     float *xs = (float *)((uint8_t *)scr + xp_bytes);
     float *part = (float *)((uint8_t *)scr + xp_bytes + xs_bytes);
-    const dim3 sgrid((n_blocks_pad * 4 + kSplitChunk - 1) / kSplitChunk, vec_pad / kSplitV);
+    const dim3 sgrid(n_splits, vec_pad / kSplitV);
     if (((uintptr_t)x & 15) == 0)  // rows start 128-byte apart: the base decides
-        hipLaunchKernelGGL(split_x_kernel<true>, sgrid, dim3(kSplitThreads), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad,
-                           xp, xs);
+        hipLaunchKernelGGL(split_x_kernel<true>, sgrid, dim3(kSplitThreads), 0, ctx->stream, x, n_vec, w->cols,
+                           n_blocks_pad, ps, vec_pad, xp, xs);
     else
-        hipLaunchKernelGGL(split_x_kernel<false>, sgrid, dim3(kSplitThreads), 0, ctx->stream, x, n_vec, w->cols, n_blocks_pad,
-                           xp, xs);
+        hipLaunchKernelGGL(split_x_kernel<false>, sgrid, dim3(kSplitThreads), 0, ctx->stream, x, n_vec, w->cols,
+                           n_blocks_pad, ps, vec_pad, xp, xs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(GLA_ERR_KERNEL, "split_x_kernel launch: %s", hipGetErrorString(e));
     // K slices summed in the split-K kernel by each row group's last workgroup
@@ -820,16 +840,20 @@ int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, f
         float *out = n_splits > 1 ? part : yv;
         switch (nvt) {
         case 1:
-            rc = launch_splitk<1>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv, arrivals);
+            rc = launch_splitk<1>(ctx, w, xp, xs, vec_pad, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv,
+                                 arrivals);
             break;
         case 2:
-            rc = launch_splitk<2>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv, arrivals);
+            rc = launch_splitk<2>(ctx, w, xp, xs, vec_pad, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv,
+                                 arrivals);
             break;
         case 3:
-            rc = launch_splitk<3>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv, arrivals);
+            rc = launch_splitk<3>(ctx, w, xp, xs, vec_pad, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv,
+                                 arrivals);
             break;
         default:
-            rc = launch_splitk<4>(ctx, w, xp, xs, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv, arrivals);
+            rc = launch_splitk<4>(ctx, w, xp, xs, vec_pad, n_blocks_pad, v0, n_vec, n_splits, out, split_stride, yv,
+                                 arrivals);
         }
         if (rc != GLA_OK) return rc;
     }

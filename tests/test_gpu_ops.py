@@ -109,7 +109,7 @@ def test_matvec_q8_0_reference_fixture(backend):
 def test_matvec_q8_0_matches_oracle_and_f64(backend, rows, cols, n_vec):
     raw = _q8_rows(rows, cols, 1300 + rows + n_vec)
     x = synth.normal(1400 + cols + n_vec, (n_vec, cols))
-    x[0, :7] *= 1e4     # a few large entries: the per-vector piece scale follows the largest
+    x[0, :7] *= 1e4     # a few large entries: the first K slice's piece scale follows the largest
     got = _matvec_gpu(backend, raw, rows, cols, x)
     wd = _dequant(raw, rows, cols)
     exact = x.astype(np.float64) @ wd.T

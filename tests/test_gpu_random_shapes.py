@@ -200,7 +200,14 @@ def test_matvec_random_shapes(backend, case):
     rows, cols, n_vec = c_["rows"], c_["cols"], c_["n_vec"]
     raw = orc.q8_quantize_rows(synth.normal_rows(99900 + case, rows, cols)).reshape(-1)
     x = synth.normal(99950 + case, (n_vec, cols))
-    x[:, : 1 + case % 5] *= 300.0   # a few large entries: each vector's piece scale follows its largest
+    # the activation pieces take a scale per vector and K slice from the slice's largest |x|:
+    # a few large entries in the first slice, and by case an all-zero stretch (a slice of
+    # zeros) or a tail a million times smaller (its slices' scales 2^20 apart from the first's)
+    x[:, : 1 + case % 5] *= 300.0
+    if case % 3 == 0:
+        x[:, cols // 2: cols // 2 + max(32, cols // 4)] = 0.0
+    elif case % 3 == 1:
+        x[:, cols // 2:] *= 1e-6
     w = backend.create_q8_weights(raw, rows, cols)
     pad = 1 if c_["misaligned"] else 0
     dx = backend.buffer(np.concatenate([np.zeros(pad, np.float32), x.reshape(-1)]))
