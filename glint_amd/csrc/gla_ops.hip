@@ -191,19 +191,26 @@ __global__ __launch_bounds__(kSplitThreads) void split_x_kernel(const float *x, 
             for (int j = 0; j < 8; j++) e[j] = src[j];
         }
     };
+    // the largest finite |x|: an infinity keeps its own piece (hi = +-inf,
+    // lo = 0) and must not push the finite ones past the f16 range; a NaN
+    // stays NaN in its pieces (the reference's block sums give inf / NaN the same way)
+    auto finite_max = [](float m, float v) {
+        const float a = fabsf(v);
+        return a <= 3.402823466e38f ? fmaxf(m, a) : m;
+    };
     float e[kSplitU][8];
     float mx = 0.0f;
 #pragma unroll
     for (int k = 0; k < kSplitU; k++) {
         load_unit(e[k], u0 + k * kSplitStep + ut);
 #pragma unroll
-        for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(e[k][j]));
+        for (int j = 0; j < 8; j++) mx = finite_max(mx, e[k][j]);
     }
     for (int u = u0 + kSplitU * kSplitStep + ut; u < uin; u += kSplitStep) {  // the rest of a wide slice
         float t[8];
         load_unit(t, u);
 #pragma unroll
-        for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(t[j]));
+        for (int j = 0; j < 8; j++) mx = finite_max(mx, t[j]);
     }
     // maximum over the threads of the same vector: lanes of equal t & 3 in
     // the wave, then the waves
@@ -216,8 +223,8 @@ __global__ __launch_bounds__(kSplitThreads) void split_x_kernel(const float *x, 
 #pragma unroll
     for (int w = 1; w < NW; w++) mx = fmaxf(mx, red[w][vq]);
     int ex = 0;
-    if (mx > 0.0f && isfinite(mx)) frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
-    const int sh = 14 - ex;                            // the largest |x| * 2^sh lies in [2^13, 2^14)
+    if (mx > 0.0f) frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+    const int sh = 14 - ex;            // the largest finite |x| * 2^sh lies in [2^13, 2^14)
     const float mul = ldexpf(1.0f, sh);
     if (threadIdx.x < kSplitV) xs[(int64_t)blockIdx.x * vec_pad + v] = ldexpf(1.0f, -sh);
     auto put = [&](const float (&t8)[8], int u) {
@@ -227,7 +234,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_x_kernel(const float *x, 
             const float t = t8[j] * mul;
             const _Float16 h = (_Float16)t;
             hi[j] = h;
-            lo[j] = (_Float16)(t - (float)h);
+            lo[j] = __builtin_isinf(t) ? (_Float16)0.0f : (_Float16)(t - (float)h);
         }
         const int blk = u >> 2;
         const int ln = (u & 3) * 16 + (v & 15);

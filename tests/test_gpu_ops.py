@@ -120,6 +120,39 @@ def test_matvec_q8_0_matches_oracle_and_f64(backend, rows, cols, n_vec):
         assert np.all(np.abs(got[v] - want) <= 4e-6 * mag[v]), v
 
 
+@pytest.mark.parametrize("n_vec", [1, 8])
+def test_matvec_q8_0_nonfinite_activations_like_the_reference(backend, n_vec):
+    """Infinite and NaN activations give what the reference's block loop gives
+    (src/tensor/quantized.rs:587-610: each block's sum of q * x, times the block's scale): +-inf
+    where the infinite terms of a row share one sign, NaN where they differ, where a zero q or
+    scale meets an infinity, or where the row holds a NaN; the same inf / NaN pattern, sign for
+    sign, as the oracle. One vector takes the vector-ALU kernel, eight the MFMA path, whose
+    activation pieces keep an infinity exact (hi = +-inf, lo = 0) and take their scale from the
+    finite entries; its finite vectors stay within the usual bar."""
+    rows, cols = 64, 512
+    raw = _q8_rows(rows, cols, 1500 + n_vec)
+    x = synth.normal(1600 + n_vec, (n_vec, cols))
+    x[0, 37] = np.inf
+    x[0, 400] *= 1e3   # a large finite entry in another K slice
+    if n_vec > 1:
+        x[1, 100] = -np.inf
+        x[1, 101] = 50.0   # beside the infinity, in its slice: must not overflow its f16 pieces
+        x[2, 5] = np.nan
+        x[3, 3] = np.inf
+        x[3, 300] = -np.inf
+    got = _matvec_gpu(backend, raw, rows, cols, x)
+    wd = _dequant(raw, rows, cols)
+    for v in range(n_vec):
+        want = orc.matvec_q8_0(raw, rows, cols, x[v])
+        np.testing.assert_array_equal(np.isnan(got[v]), np.isnan(want), err_msg=f"vector {v}")
+        np.testing.assert_array_equal(np.isposinf(got[v]), np.isposinf(want), err_msg=f"vector {v}")
+        np.testing.assert_array_equal(np.isneginf(got[v]), np.isneginf(want), err_msg=f"vector {v}")
+        if np.all(np.isfinite(x[v])):
+            mag = np.abs(x[v].astype(np.float64)) @ np.abs(wd).T
+            assert np.all(np.abs(got[v] - want) <= 4e-6 * mag), v
+    assert not np.all(np.isfinite(got[0]))
+
+
 def test_ops_argument_errors_and_empty_calls(backend):
     """Shapes the ABI rejects come back as GLA_ERR_INVALID (the caller's CPU path), and empty
     calls are no-ops: zero vectors, zero rows, a rotary dimension of 0 or 1 (no whole pair)."""
