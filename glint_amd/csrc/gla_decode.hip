@@ -246,7 +246,7 @@ __device__ __forceinline__ void merge_splits_agent(const DecodeParams &p, int64_
 #pragma unroll
     for (int k = 0; k < EPT; k++) {
         const int idx = tid + k * kThreads;
-        if (idx < n_el) out[idx] = L[k] > 0.0f ? A[k] * (1.0f / L[k]) : 0.0f;
+        if (idx < n_el) out[idx] = L[k] > 0.0f ? A[k] * (1.0f / L[k]) : A[k];  // (a NaN sum stays NaN, as flash.rs:118-123)
     }
 }
 
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(const DecodePara
             A = fmaf(lds_acc[w][g][e], f, A);
         }
         if (r.n_splits == 1) {
-            p.out[((int64_t)b * p.n_heads + h_base + g) * D + e] = L > 0.0f ? A * (1.0f / L) : 0.0f;
+            p.out[((int64_t)b * p.n_heads + h_base + g) * D + e] = L > 0.0f ? A * (1.0f / L) : A;
         } else {
             const int64_t slot = unit * p.max_splits + split;
             if (arrive)
@@ -547,14 +547,20 @@ __global__ __launch_bounds__(kThreads) void decode_combine_kernel(const DecodePa
             const int s = s0 + j * NSG;
             const int sc = s < r.n_splits ? s : s0;
             const int64_t slot = (slot0 + sc) * GT + g;
-            mi[j] = s < r.n_splits ? p.part_ml[(slot0 + sc) * 32 + g] : -INFINITY;
-            li[j] = p.part_ml[(slot0 + sc) * 32 + 8 + g];
-            ai[j] = reinterpret_cast<const float4 *>(p.part_acc + slot * D)[e4];
+            const bool in = s < r.n_splits;
+            const float lv = p.part_ml[(slot0 + sc) * 32 + 8 + g];
+            const float4 av = reinterpret_cast<const float4 *>(p.part_acc + slot * D)[e4];
+            // an entry past the last split reloads split s0 and adds nothing
+            // (not 0 x its sums: an infinity there would make NaN)
+            mi[j] = in ? p.part_ml[(slot0 + sc) * 32 + g] : -INFINITY;
+            li[j] = in ? lv : 0.0f;
+            ai[j] = in ? av : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
         float bm = M;
 #pragma unroll
         for (int j = 0; j < BATCH; j++) bm = fmaxf(bm, mi[j]);
-        if (bm == -INFINITY) continue;
+        // (no skip when every m is -inf: a split whose scores were all NaN has
+        // m = -inf and NaN sums, and they reach the output, as the reference's do)
         const float f0 = (M == -INFINITY) ? 0.0f : fast_exp2(M - bm);
         L *= f0;
         A.x *= f0;

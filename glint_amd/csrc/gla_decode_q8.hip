@@ -830,8 +830,8 @@ __device__ __forceinline__ void q8_item(const Q8Params &p, uint8_t (*slots)[kSlo
         for (int w = 0; w < kWaves; w++) Mg = fmaxf(Mg, res(w, tid, D));
 #pragma unroll
         for (int w = 0; w < kWaves; w++) {
-            const float mw = res(w, tid, D);
-            if (mw != -INFINITY) Lg = fmaf(res(w, tid, D + 1), fast_exp2(mw - Mg), Lg);
+            const float mw = res(w, tid, D), lw = res(w, tid, D + 1);
+            if (mw != -INFINITY || lw != 0.0f) Lg = fmaf(lw, mw == -INFINITY ? 0.0f : fast_exp2(mw - Mg), Lg);
         }
     }
     for (int i4 = tid; i4 < kGT * D / 4; i4 += kThreads) {
@@ -842,11 +842,15 @@ __device__ __forceinline__ void q8_item(const Q8Params &p, uint8_t (*slots)[kSlo
         for (int w = 0; w < kWaves; w++) M = fmaxf(M, res(w, g, D));
         float L = 0.0f;
         float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        // A wave with no pages leaves m = -inf, l = 0 and its sums unwritten:
+        // it is skipped. A wave whose scores were all NaN has m = -inf and
+        // NaN l and sums: it enters with weight 0, so the NaN reaches the
+        // output, as the reference's does.
 #pragma unroll
         for (int w = 0; w < kWaves; w++) {
             const float mw = res(w, g, D);
-            if (mw != -INFINITY) {
-                const float f = fast_exp2(mw - M);
+            if (mw != -INFINITY || res(w, g, D + 1) != 0.0f) {
+                const float f = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
                 L = fmaf(res(w, g, D + 1), f, L);
                 A.x = fmaf(res(w, g, d + 0), f, A.x);
                 A.y = fmaf(res(w, g, d + 1), f, A.y);
@@ -936,14 +940,20 @@ __global__ __launch_bounds__(kGT * D / 4) void decode_q8_combine_kernel(const Q8
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int i = min(i0 + j, n_wg - 1);
-            mi[j] = (i0 + j < n_wg) ? hp[i * pstride + kGT * D + g] : -INFINITY;
-            li[j] = hp[i * pstride + kGT * D + kGT + g];
-            ai[j] = *reinterpret_cast<const float4 *>(hp + i * pstride + g * D + d);
+            const bool in = i0 + j < n_wg;
+            const float lv = hp[i * pstride + kGT * D + kGT + g];
+            const float4 av = *reinterpret_cast<const float4 *>(hp + i * pstride + g * D + d);
+            // an entry past the last partial reloads the last one and adds
+            // nothing (not 0 x its sums: an infinity there would make NaN)
+            mi[j] = in ? hp[i * pstride + kGT * D + g] : -INFINITY;
+            li[j] = in ? lv : 0.0f;
+            ai[j] = in ? av : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
         float bm = M;
 #pragma unroll
         for (int j = 0; j < 8; j++) bm = fmaxf(bm, mi[j]);
-        if (bm == -INFINITY) continue;
+        // (no skip when every m is -inf: a partial whose scores were all NaN
+        // has m = -inf and NaN sums, and they reach the output, as the reference's do)
         const float f0 = (M == -INFINITY) ? 0.0f : fast_exp2(M - bm);
         L *= f0;
         A.x *= f0;
@@ -961,9 +971,11 @@ __global__ __launch_bounds__(kGT * D / 4) void decode_q8_combine_kernel(const Q8
         }
         M = bm;
     }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    // (L not > 0: no weight reached the head, or a NaN did; A is then 0 or NaN
+    // and is written as it is, as flash.rs:118-123 leaves the sums unnormalised)
+    const float inv = L > 0.0f ? 1.0f / L : 1.0f;
     *reinterpret_cast<float4 *>(p.out + ((int64_t)b * p.n_heads + h_base + g) * D + d) =
-        L > 0.0f ? make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
 }
 
 template <int D>

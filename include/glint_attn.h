@@ -186,7 +186,11 @@ long gla_window_start(long pos, long sliding_window, int alternating, int layer)
  * KV, K/V head h / (n_heads / n_kv_heads), cap(s) = softcap * tanh(s / softcap)
  * when softcap > 0 -- flash_attn_1d_ext per head (src/tensor/flash.rs:46-124)
  * as attn_heads_cpu calls it (src/transformer/forward.rs:240-270). kv_len 0
- * gives a zero output, as the reference's pre-zeroed buffer does.
+ * gives a zero output, as the reference's pre-zeroed buffer does. Non-finite
+ * data behaves as there: a NaN reaching a head's weights or sums makes the
+ * head's output NaN (the reference leaves such sums unnormalised,
+ * flash.rs:118-123), and an infinite value under a non-zero weight gives
+ * +-inf in its dimension.
  *
  * Out-of-range indices. The reference panics on a position or page id
  * outside the storage (Vec indexing in PagedKvCache::read_k_head,
