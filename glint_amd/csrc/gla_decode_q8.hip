@@ -658,7 +658,10 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
         for (int s = 0; s < 8; s++) {
             const float x = t[s] * p.q_mul;
             qx[blk][s] = x;
-            qmax = fmaxf(qmax, fabsf(x));
+            // the largest finite |q|: an infinite entry keeps its own pieces
+            // (hi = +-inf, lo = 0), so its scores are +-inf as the reference's are
+            const float a = fabsf(x);
+            qmax = a <= 3.402823466e38f ? fmaxf(qmax, a) : qmax;
         }
     }
     qmax = max_rows(qmax);
@@ -671,7 +674,7 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
         for (int s = 0; s < 8; s++) {
             const float x = qx[blk][s] * qs;
             const _Float16 hi = (_Float16)x;
-            const _Float16 lo = (_Float16)(x - (float)hi);
+            const _Float16 lo = __builtin_isinf(x) ? (_Float16)0.0f : (_Float16)(x - (float)hi);
             const bool mine = qvalid && ((blk & 1) == ph);
             c.qb[blk][s] = mine ? (piece ? lo : hi) : (_Float16)0.0f;
         }

@@ -5,7 +5,8 @@ head's output is NaN, not zeros; an infinite value under a non-zero weight gives
 dimension; an infinite q entry gives infinite or NaN scores. Every path is checked: f32 decode
 through the split kernel's in-kernel merge and through the combine kernel, Q8_0 decode (whose
 codec turns a block holding a NaN or an infinity into NaN or infinite values, as the reference
-codec does) through one workgroup and through the combine, and fp32 and bf16-input prefill.
+codec does) through one workgroup and through the combine, and fp32 and bf16-input prefill,
+each with and without the soft-cap (under which an infinite score becomes +-cap).
 The inf / NaN pattern must equal the oracle's element for element, sign for sign, and the
 finite elements stay within the usual bars."""
 from __future__ import annotations
@@ -49,8 +50,9 @@ def _check(got, want, tol_abs, tol_rel, what):
     assert np.all(ok), f"{what}: finite elements off by up to {float(err.max())}"
 
 
+@pytest.mark.parametrize("cap", [None, 30.0])
 @pytest.mark.parametrize("dtype", ["f32", "q8"])
-def test_decode_nonfinite_like_reference(backend, dtype):
+def test_decode_nonfinite_like_reference(backend, dtype, cap):
     B, max_seq = 6, 2048
     k = synth.normal_rows(71, B * max_seq, HKV * D).reshape(B, 1, max_seq, HKV * D)
     v = synth.normal_rows(72, B * max_seq, HKV * D).reshape(B, 1, max_seq, HKV * D)
@@ -65,19 +67,21 @@ def test_decode_nonfinite_like_reference(backend, dtype):
     kv_len = np.array([200, 200, 200, 200, 2000, 2000], np.int32)
     scale = 1 / np.sqrt(D)
     want = orc.decode_batch(q.reshape(B, H * D), c.stores, 0, kv_start, kv_len, H, HKV, D, scale,
-                            None).reshape(B, H, D)
+                            cap).reshape(B, H, D)
     # (the Q8_0 codec drops a NaN, quantised to 0, and makes a block holding an infinity NaN)
     if dtype == "f32":
         assert np.isnan(want[0, :GROUP]).all() and np.isposinf(want[1, GROUP:, 3]).all()
     else:
         assert np.isfinite(want[0]).all() and np.isnan(want[1, GROUP:, :32]).all()
-    assert np.isnan(want[3, 5]).all() and np.isfinite(want[3, :5]).all()
-    got = run_decode(backend, c.cache, q, kv_start, kv_len, H, scale)
-    _check(got, want, ABS_TOL, REL_TOL, f"{dtype} decode")
+    # (under the soft-cap an infinite score becomes +-cap: that head's output is finite)
+    assert np.isfinite(want[3, :5]).all() and (np.isfinite(want[3, 5]).all() if cap else np.isnan(want[3, 5]).all())
+    got = run_decode(backend, c.cache, q, kv_start, kv_len, H, scale, cap)
+    _check(got, want, ABS_TOL, REL_TOL, f"{dtype} decode, cap {cap}")
 
 
+@pytest.mark.parametrize("cap", [None, 30.0])
 @pytest.mark.parametrize("precision", ["f32", "bf16"])
-def test_prefill_nonfinite_like_reference(backend, precision):
+def test_prefill_nonfinite_like_reference(backend, precision, cap):
     B, max_seq, n_q = 4, 256, 64
     k = synth.normal_rows(81, B * max_seq, HKV * D).reshape(B, 1, max_seq, HKV * D)
     v = synth.normal_rows(82, B * max_seq, HKV * D).reshape(B, 1, max_seq, HKV * D)
@@ -90,7 +94,7 @@ def test_prefill_nonfinite_like_reference(backend, precision):
     scale = 1 / np.sqrt(D)
     want = np.concatenate([
         orc.prefill(q[b * n_q:(b + 1) * n_q].reshape(n_q, H * D), c.stores[b], 0, 100, H, HKV, D, scale,
-                    None, None).reshape(n_q, H, D) for b in range(B)])
-    got = run_prefill(backend, c.cache, q, q_start, pos_offset, H, scale, precision=precision)
+                    cap, None).reshape(n_q, H, D) for b in range(B)])
+    got = run_prefill(backend, c.cache, q, q_start, pos_offset, H, scale, cap, precision=precision)
     tol = (ABS_TOL, REL_TOL) if precision == "f32" else (3e-2, 3e-2)
-    _check(got, want, tol[0], tol[1], f"{precision} prefill")
+    _check(got, want, tol[0], tol[1], f"{precision} prefill, cap {cap}")
