@@ -98,3 +98,66 @@ def test_prefill_nonfinite_like_reference(backend, precision, cap):
     got = run_prefill(backend, c.cache, q, q_start, pos_offset, H, scale, cap, precision=precision)
     tol = (ABS_TOL, REL_TOL) if precision == "f32" else (3e-2, 3e-2)
     _check(got, want, tol[0], tol[1], f"{precision} prefill, cap {cap}")
+
+
+def _plant_outside(k, v, lo, hi):
+    """NaN in K and +-inf / NaN in V at every KV head of positions lo-3 .. lo-1 and hi .. hi+2
+    (the slots just outside a window, in the same pages and tiles as its edges)."""
+    for pos in list(range(max(0, lo - 3), lo)) + list(range(hi, min(k.shape[2], hi + 3))):
+        k[:, 0, pos, ::7] = np.nan
+        v[:, 0, pos, ::5] = np.inf
+        v[:, 0, pos, 1::5] = -np.inf
+        v[:, 0, pos, 2::5] = np.nan
+
+
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+def test_decode_ignores_nonfinite_outside_the_window(backend, dtype):
+    """Slots outside [kv_start, kv_start + kv_len) are never read by the reference: non-finite
+    data there, in the same pages as the window's edges, must not reach the output."""
+    B, max_seq = 2, 2048
+    starts = np.array([21, 37], np.int32)
+    lens = np.array([150, 1900], np.int32)  # the split kernel's own merge, and the combine
+    k = synth.normal_rows(91, B * max_seq, HKV * D).reshape(B, 1, max_seq, HKV * D)
+    v = synth.normal_rows(92, B * max_seq, HKV * D).reshape(B, 1, max_seq, HKV * D)
+    for b in range(B):
+        kb, vb = k[b:b + 1], v[b:b + 1]
+        _plant_outside(kb, vb, int(starts[b]), int(starts[b] + lens[b]))
+    c = Contig(backend, dtype, B, 1, max_seq, HKV, D, k=k, v=v)
+    q = synth.normal(93, (B, H, D))
+    for cap in (None, 30.0):
+        want = orc.decode_batch(q.reshape(B, H * D), c.stores, 0, starts, lens, H, HKV, D, 0.125,
+                                cap).reshape(B, H, D)
+        assert np.isfinite(want).all()
+        got = run_decode(backend, c.cache, q, starts, lens, H, 0.125, cap)
+        _check(got, want, ABS_TOL, REL_TOL, f"{dtype} decode outside the window, cap {cap}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+@pytest.mark.parametrize("precision", ["f32", "bf16"])
+def test_prefill_ignores_nonfinite_outside_the_window(backend, precision, dtype):
+    """Keys after a sequence's last query position, and before its sliding window, sit in the
+    tiles prefill reads but are never attended: non-finite data there must not reach the output
+    (a masked weight times a NaN value would still be NaN)."""
+    B, max_seq, n_q, window = 2, 512, 70, 40
+    k = synth.normal_rows(95, B * max_seq, HKV * D).reshape(B, 1, max_seq, HKV * D)
+    v = synth.normal_rows(96, B * max_seq, HKV * D).reshape(B, 1, max_seq, HKV * D)
+    pos0 = 101
+    # first attended key: pos0 - window + 1 with the window, 0 without; last: pos0 + n_q - 1
+    _plant_outside(k, v, pos0 - window + 1, pos0 + n_q)
+    c = Contig(backend, dtype, B, 1, max_seq, HKV, D, k=k, v=v)
+    q = synth.normal(97, (B * n_q, H, D))
+    q_start = np.arange(B + 1, dtype=np.int32) * n_q
+    pos_offset = np.full(B, pos0, np.int32)
+    tol = (ABS_TOL, REL_TOL) if precision == "f32" else (3e-2, 3e-2)
+    for sw in (window, None):
+        if sw is None:  # no window: the slots before it are attended, so only the tail stays planted
+            k2, v2 = k.copy(), v.copy()
+            k2[:, 0, : pos0 - window + 1] = k[:, 0, 200:200 + pos0 - window + 1]
+            v2[:, 0, : pos0 - window + 1] = v[:, 0, 200:200 + pos0 - window + 1]
+            c = Contig(backend, dtype, B, 1, max_seq, HKV, D, k=k2, v=v2)
+        want = np.concatenate([
+            orc.prefill(q[b * n_q:(b + 1) * n_q].reshape(n_q, H * D), c.stores[b], 0, pos0, H, HKV, D, 0.125,
+                        None, sw).reshape(n_q, H, D) for b in range(B)])
+        assert np.isfinite(want).all()
+        got = run_prefill(backend, c.cache, q, q_start, pos_offset, H, 0.125, None, sw, precision=precision)
+        _check(got, want, tol[0], tol[1], f"{precision} prefill over {dtype}, window {sw}")
