@@ -153,6 +153,26 @@ def test_matvec_q8_0_nonfinite_activations_like_the_reference(backend, n_vec):
     assert not np.all(np.isfinite(got[0]))
 
 
+def test_matvec_q8_0_result_independent_of_the_batch(backend):
+    """A vector's outputs do not depend on the other vectors of the call, as in the reference,
+    which computes each vector alone (src/tensor/quantized.rs:247-346): on the MFMA path (5 or
+    more vectors) every output's arithmetic order is fixed by the shape, and a piece scale by the
+    vector's own slice, so the first vectors come out bit for bit the same in batches of 5, 17,
+    64 and 70 (two launches). Batches of 1-4 take the vector-ALU kernel, whose rounding differs:
+    those agree with the MFMA path within the matvec bar."""
+    rows, cols = 200, 1536
+    raw = _q8_rows(rows, cols, 1700)
+    x = synth.normal(1701, (70, cols))
+    x[1, 5] *= 1e4  # an outlier in vector 1: the other vectors' piece scales must not follow it
+    base = _matvec_gpu(backend, raw, rows, cols, x[:5])
+    for n in (17, 64, 70):
+        got = _matvec_gpu(backend, raw, rows, cols, x[:n])
+        assert np.array_equal(got[:5].view(np.uint32), base.view(np.uint32)), n
+    few = _matvec_gpu(backend, raw, rows, cols, x[:3])
+    mag = np.abs(x[:3].astype(np.float64)) @ np.abs(_dequant(raw, rows, cols)).T
+    assert np.all(np.abs(few - base[:3]) <= 4e-6 * mag)
+
+
 def test_ops_argument_errors_and_empty_calls(backend):
     """Shapes the ABI rejects come back as GLA_ERR_INVALID (the caller's CPU path), and empty
     calls are no-ops: zero vectors, zero rows, a rotary dimension of 0 or 1 (no whole pair)."""
