@@ -12,6 +12,8 @@ bit for bit. Alone, the Q8_0 path spreads the q-heads of a KV head over more wav
 too small to fill the device otherwise), so this also checks that a head's result does not
 depend on the heads that share its wave. For f32 the host-buffer entry point
 (GpuBackend::attention, Glint's [pos][kv_head][d] layout) must give the same bits as well.
+Prefill keeps the same property: a prompt gives the same bits alone, in a ragged batch and in a
+shuffled sub-batch, on both the fp32 and the bf16-input paths.
 """
 from __future__ import annotations
 
@@ -109,3 +111,35 @@ def test_f32_merge_switch_is_batch_invariant(backend, d, h, hkv, nb):
         alone = run_decode(backend, c.cache, q[b:b + 1], starts[b:b + 1], lens[b:b + 1], h, scale,
                            seq_slot=[b])
         assert np.array_equal(_bits(alone[0]), _bits(full[b])), f"seq {b} (start {starts[b]}, len {lens[b]}) alone"
+
+
+@pytest.mark.parametrize("precision", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "q8"])
+def test_prefill_is_batch_invariant(backend, dtype, precision):
+    """A prompt's prefill gives the same bits alone as in a ragged batch of prompts (different
+    lengths and position offsets, so the grid, the query-block count and the staged tile images
+    are sized by other sequences), global and with a 48-token sliding window and soft-cap 30."""
+    from gpu_util import Contig, run_prefill
+
+    h, hkv, d = 8, 2, 64
+    lens = np.array([70, 1, 129, 33], np.int32)
+    offs = np.array([0, 200, 17, 300], np.int32)
+    max_seq = 512
+    c = Contig(backend, dtype, len(lens), 1, max_seq, hkv, d, seed=4101, k_mul=3.0)
+    q = synth.normal(4102, (int(lens.sum()), h, d))
+    q_start = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    for sw, cap in ((None, None), (48, 30.0)):
+        whole = run_prefill(backend, c.cache, q, q_start, offs, h, 0.125, cap, sw, precision=precision)
+        for b in range(len(lens)):
+            rows = slice(int(q_start[b]), int(q_start[b + 1]))
+            alone = run_prefill(backend, c.cache, q[rows], np.array([0, lens[b]], np.int32), offs[b:b + 1], h, 0.125,
+                                cap, sw, precision=precision, seq_slot=np.array([b], np.int32))
+            assert np.array_equal(_bits(alone), _bits(whole[rows])), (dtype, precision, sw, b)
+        order = [2, 0, 3]  # a shuffled sub-batch
+        sub_q = np.concatenate([q[int(q_start[b]):int(q_start[b + 1])] for b in order])
+        sub_start = np.concatenate([[0], np.cumsum(lens[order])]).astype(np.int32)
+        sub = run_prefill(backend, c.cache, sub_q, sub_start, offs[order], h, 0.125, cap, sw, precision=precision,
+                          seq_slot=np.array(order, np.int32))
+        for i, b in enumerate(order):
+            assert np.array_equal(_bits(sub[int(sub_start[i]):int(sub_start[i + 1])]),
+                                  _bits(whole[int(q_start[b]):int(q_start[b + 1])])), (dtype, precision, sw, "sub", b)
