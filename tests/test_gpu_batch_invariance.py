@@ -143,3 +143,24 @@ def test_prefill_is_batch_invariant(backend, dtype, precision):
         for i, b in enumerate(order):
             assert np.array_equal(_bits(sub[int(sub_start[i]):int(sub_start[i + 1])]),
                                   _bits(whole[int(q_start[b]):int(q_start[b + 1])])), (dtype, precision, sw, "sub", b)
+
+
+@pytest.mark.parametrize("precision", ["f32", "bf16"])
+def test_chunked_prefill_equals_one_pass(backend, precision):
+    """A prompt prefilled in chunks (the second continuing at the first's end) gives the same
+    bits as one pass: in the reference each query runs the same blocked softmax over keys
+    0 .. its position whichever call it belongs to (src/transformer/forward.rs:927-958)."""
+    from gpu_util import Contig, run_prefill
+
+    h, hkv, d, n = 8, 2, 64, 150
+    c = Contig(backend, "f32", 1, 1, 256, hkv, d, seed=4201)
+    q = synth.normal(4202, (n, h, d))
+    for sw in (None, 40):
+        one = run_prefill(backend, c.cache, q, np.array([0, n], np.int32), np.array([0], np.int32), h, 0.125,
+                          None, sw, precision=precision)
+        for cut in (70, 97):
+            a = run_prefill(backend, c.cache, q[:cut], np.array([0, cut], np.int32), np.array([0], np.int32), h,
+                            0.125, None, sw, precision=precision)
+            b = run_prefill(backend, c.cache, q[cut:], np.array([0, n - cut], np.int32), np.array([cut], np.int32), h,
+                            0.125, None, sw, precision=precision)
+            assert np.array_equal(_bits(np.concatenate([a, b])), _bits(one)), (precision, sw, cut)
