@@ -809,6 +809,10 @@ int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, f
         }
         return rc;
     }
+    // split_x_kernel's grid takes 4 vectors per row, at most 65,535 rows
+    constexpr int kMaxVec = 65535 * kSplitV / 16 * 16;
+    if (n_vec > kMaxVec)
+        return set_error(GLA_ERR_INVALID, "gla_matvec_q8_0: n_vec %d > %d (split the call)", n_vec, kMaxVec);
     const int n_blocks_pad = 2 * w->n_pairs;
     const int vec_pad = (n_vec + 15) / 16 * 16;
     const int n_groups = (w->n_tiles + kSkRT - 1) / kSkRT;

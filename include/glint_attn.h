@@ -343,7 +343,7 @@ int gla_q8w_cols(const gla_q8w *w);
  * and matvec_batch over Q8_0 (src/tensor/quantized.rs:247-346, :587-610; the
  * wgpu matvec_q8_0 shader's job). x device [n_vec][cols], y device
  * [n_vec][rows], f32. Asynchronous; the weights are read once per 64
- * vectors. */
+ * vectors. n_vec above 262,128 is refused (GLA_ERR_INVALID): split the call. */
 int gla_matvec_q8_0(gla_ctx *ctx, const gla_q8w *w, const float *x, int n_vec, float *y);
 
 #ifdef __cplusplus

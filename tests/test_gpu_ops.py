@@ -190,6 +190,11 @@ def test_ops_argument_errors_and_empty_calls(backend):
     with pytest.raises(GlaError) as e:
         backend.matvec_q8_0(w, backend.empty(64 * 4), -1, y)
     assert e.value.code == GLA_ERR_INVALID
+    with pytest.raises(GlaError) as e:  # past the activation split's grid: refused before any launch
+        backend.matvec_q8_0(w, backend.empty(64 * 4), 262129, y)
+    assert e.value.code == GLA_ERR_INVALID and "n_vec" in str(e.value)
+    backend.matvec_q8_0(w, backend.empty(64 * 4), 0, y)  # and the context still works
+    backend.sync()
     w.destroy()
 
     x = synth.normal(3, (2, 2, 8))
