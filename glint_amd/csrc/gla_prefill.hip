@@ -1333,12 +1333,13 @@ int launch_prefill(gla_ctx *ctx, const PrefillLaunch &a) {
         return set_error(GLA_ERR_INVALID, "unsupported head_dim %d", D);
     }
     // bf16: the staged path keeps the bf16 tile images of every (sequence, KV
-    // head) in scratch, up to 1 GiB; beyond that each workgroup converts its
-    // own tiles (prefill_bf16_kernel)
+    // head) in scratch, up to 1 GiB, and its staging grid has one z row per
+    // sequence (at most 65,535); beyond either each workgroup converts its own
+    // tiles (prefill_bf16_kernel, the same bits)
     const int n_tiles = (a.pm.pos_limit + KT - 1) / KT;
     const size_t img_bytes = (size_t)a.n_seqs * a.n_kv_heads * (size_t)n_tiles * (size_t)(128 * D);
     const bool staged = a.precision == GLA_PREC_BF16 && getenv("GLA_BF16_UNSTAGED") == nullptr && n_tiles > 0 &&
-                        img_bytes <= ((size_t)1 << 30);
+                        img_bytes <= ((size_t)1 << 30) && a.n_seqs <= 65535;
     if (a.precision == GLA_PREC_BF16) {
         NT = 2;
         if (staged)
