@@ -658,13 +658,26 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
         for (int s = 0; s < 8; s++) {
             const float x = t[s] * p.q_mul;
             qx[blk][s] = x;
-            // the largest finite |q|: an infinite entry keeps its own pieces
-            // (hi = +-inf, lo = 0), so its scores are +-inf as the reference's are
-            const float a = fabsf(x);
-            qmax = a <= 3.402823466e38f ? fmaxf(qmax, a) : qmax;
+            qmax = fmaxf(qmax, fabsf(x));
         }
     }
     qmax = max_rows(qmax);
+    // An infinite q entry (a wave-uniform branch, so finite q pays nothing for
+    // it): the scale comes from the finite entries and the infinity keeps its
+    // own pieces exact (hi = +-inf, lo = 0), so its scores are +-inf, or +-cap
+    // under the soft-cap, as the reference's are.
+    const bool q_inf = __ballot(!(qmax <= 3.402823466e38f)) != 0;
+    if (q_inf) {
+        float fm = 0.0f;
+#pragma unroll
+        for (int blk = 0; blk < NB; blk++)
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const float a = fabsf(qx[blk][s]);
+                fm = a <= 3.402823466e38f ? fmaxf(fm, a) : fm;
+            }
+        qmax = max_rows(fm);
+    }
     const int qe = pow2_exp(qmax);
     const float qs = ldexpf(1.0f, 14 - qe);
     StepConst<D> c;
@@ -674,10 +687,17 @@ __device__ __forceinline__ void wave_chunk(const Q8Params &p, const Range &r, in
         for (int s = 0; s < 8; s++) {
             const float x = qx[blk][s] * qs;
             const _Float16 hi = (_Float16)x;
-            const _Float16 lo = __builtin_isinf(x) ? (_Float16)0.0f : (_Float16)(x - (float)hi);
+            const _Float16 lo = (_Float16)(x - (float)hi);
             const bool mine = qvalid && ((blk & 1) == ph);
             c.qb[blk][s] = mine ? (piece ? lo : hi) : (_Float16)0.0f;
         }
+    if (q_inf) {
+#pragma unroll
+        for (int blk = 0; blk < NB; blk++)
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                if (piece && __builtin_isinf(qx[blk][s])) c.qb[blk][s] = (_Float16)0.0f;
+    }
     const float inv_qs = ldexpf(1.0f, qe - 14);
 
     float inv_vsc;
